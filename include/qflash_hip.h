@@ -1,0 +1,87 @@
+/*
+ * qflash_hip.h - C ABI of the MI355X (gfx950) integer-only attention forward.
+ *
+ * The library libqflash_hip.so replaces the two Triton kernels of
+ * EfficientCompLab/qflash and their launch ABI:
+ *   qflash_kernel[grid](Q, K, V, Out, sm_rscale, exp_M, req_M, l_M, acc_M,
+ *                       16 strides, Z, H, N_CTX=, HEAD_DIM=, EXP_USE_SHIFT=,
+ *                       L_USE_SHIFT=, ACC_USE_SHIFT=, L_SHIFT=, ACC_SHIFT=)
+ *     (qflash/kernel.py:85-104, launched at :319-326)
+ *   qflash_masked_kernel[grid](..., attn_bias, ..., 4 more strides, ...)
+ *     (qflash/kernel.py:183-203, launched at :339-346)
+ *
+ * Conventions (all entry points):
+ *   - plain C types only; device pointers come from the caller (no
+ *     allocation inside any call); strides are in elements, int64, in the
+ *     reference's order (z, h, row, col) per tensor; bias strides may be 0
+ *     (broadcast);
+ *   - the launch is asynchronous on `stream` (a hipStream_t, NULL = the
+ *     default stream); the call returns 0 or a negative QFLASH_HIP_E* code
+ *     and never throws; qflash_hip_last_error() gives a message for the
+ *     last failure on the calling thread;
+ *   - reentrant: no mutable global state besides the per-thread message.
+ */
+#ifndef QFLASH_HIP_H
+#define QFLASH_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QFLASH_HIP_OK 0
+#define QFLASH_HIP_EINVAL (-1)      /* bad pointer, shape, stride or constant */
+#define QFLASH_HIP_EHEADDIM (-2)    /* HEAD_DIM unsupported (D=16 fails BLOCK_N<=HEAD_DIM, kernel.py:105) */
+#define QFLASH_HIP_ELAUNCH (-3)     /* the HIP runtime rejected the launch */
+
+/* Arithmetic-variant switches, kernel.py:30-36 (QFLASH_* environment). */
+typedef struct qflash_hip_flags {
+    int32_t exp_use_shift; /* QFLASH_EXP_USE_SHIFT, default 1 */
+    int32_t l_use_shift;   /* QFLASH_L_USE_SHIFT, default 1 */
+    int32_t acc_use_shift; /* QFLASH_ACC_USE_SHIFT, default 1 */
+    int32_t l_shift;       /* QFLASH_L_SHIFT, default 30, 1..62 */
+    int32_t acc_shift;     /* QFLASH_ACC_SHIFT, default 30, 1..62 */
+} qflash_hip_flags;
+
+/*
+ * Unmasked integer attention forward: Out[z,h,i,:] = int8 codes of row i.
+ * Replaces qflash_kernel (qflash/kernel.py:85-180).
+ *   strides[16] = Q(z,h,m,k), K(z,h,n,k), V(z,h,k,n), Out(z,h,m,n),
+ *   exactly the order of `*query.stride(), *key.stride(), *value.stride(),
+ *   *o.stride()` at kernel.py:322.
+ */
+int qflash_hip_kernel(const int8_t* Q, const int8_t* K, const int8_t* V, int8_t* Out,
+                      int32_t sm_rscale, int32_t exp_M, int32_t req_M, int32_t l_M, int32_t acc_M,
+                      const int64_t* strides, int32_t Z, int32_t H, int32_t N_CTX, int32_t HEAD_DIM,
+                      const qflash_hip_flags* flags, void* stream);
+
+/*
+ * Masked integer attention forward with an additive int32 logit bias.
+ * Replaces qflash_masked_kernel (qflash/kernel.py:183-272).
+ *   strides[20] = the 16 above followed by attn_bias(z,h,m,n) (kernel.py:342);
+ *   bias strides may be 0 so a broadcast bias need not be materialised.
+ */
+int qflash_hip_masked_kernel(const int8_t* Q, const int8_t* K, const int8_t* V, int8_t* Out,
+                             const int32_t* attn_bias, int32_t sm_rscale, int32_t exp_M, int32_t req_M,
+                             int32_t l_M, int32_t acc_M, const int64_t* strides, int32_t Z, int32_t H,
+                             int32_t N_CTX, int32_t HEAD_DIM, const qflash_hip_flags* flags, void* stream);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* qflash_hip_last_error(void);
+
+/*
+ * Layout self-check of the int8 MFMA used by the kernels (no counterpart in
+ * the reference): C(32x32 int32) = A(32x32 int8, row-major) x B(32x32 int8,
+ * row-major), all device pointers, computed with the same operand and
+ * result register layouts the attention kernels rely on.
+ */
+int qflash_hip_mfma_layout_check(const int8_t* A, const int8_t* B, int32_t* C, void* stream);
+
+/* Library version string (no counterpart in the reference). */
+const char* qflash_hip_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QFLASH_HIP_H */

@@ -1,0 +1,84 @@
+"""ctypes binding of libqflash_hip.so (declared in include/qflash_hip.h).
+
+The product path has no fallback: if the library is missing or a call
+fails, an exception is raised.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+from ._build import LIB_PATH
+
+
+class QFlashLibraryError(RuntimeError):
+    """The HIP library is missing, failed to load, or rejected a call."""
+
+
+class QFlashCompilationError(QFlashLibraryError):
+    """HEAD_DIM the kernels cannot be built for.
+
+    The reference fails at Triton compile time for HEAD_DIM=16
+    (tl.static_assert(BLOCK_N <= HEAD_DIM), qflash/kernel.py:105,204).
+    """
+
+
+class Flags(ctypes.Structure):
+    _fields_ = [("exp_use_shift", ctypes.c_int32), ("l_use_shift", ctypes.c_int32),
+                ("acc_use_shift", ctypes.c_int32), ("l_shift", ctypes.c_int32),
+                ("acc_shift", ctypes.c_int32)]
+
+
+EXPORTS = ("qflash_hip_kernel", "qflash_hip_masked_kernel", "qflash_hip_last_error",
+           "qflash_hip_mfma_layout_check", "qflash_hip_version")
+
+E_HEADDIM = -2
+
+_lock = threading.Lock()
+_lib = None
+
+
+def _declare(L):
+    vp, i32, i64p = ctypes.c_void_p, ctypes.c_int32, ctypes.POINTER(ctypes.c_int64)
+    fp = ctypes.POINTER(Flags)
+    L.qflash_hip_kernel.restype = ctypes.c_int
+    L.qflash_hip_kernel.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i64p, i32, i32, i32, i32, fp, vp]
+    L.qflash_hip_masked_kernel.restype = ctypes.c_int
+    L.qflash_hip_masked_kernel.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i64p, i32, i32, i32, i32,
+                                           fp, vp]
+    L.qflash_hip_last_error.restype = ctypes.c_char_p
+    L.qflash_hip_last_error.argtypes = []
+    L.qflash_hip_mfma_layout_check.restype = ctypes.c_int
+    L.qflash_hip_mfma_layout_check.argtypes = [vp, vp, vp, vp]
+    L.qflash_hip_version.restype = ctypes.c_char_p
+    L.qflash_hip_version.argtypes = []
+
+
+def load(path: str | None = None):
+    """Load (once) and return the library; raise if it is not built."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = path or os.environ.get("QFLASH_HIP_LIB", LIB_PATH)
+        if not os.path.exists(path):
+            raise QFlashLibraryError(
+                f"{path} is not built: run `python -m qflash_amd._build` (or __graft_entry__.build()) first")
+        try:
+            L = ctypes.CDLL(path)
+        except OSError as e:  # pragma: no cover - depends on the box
+            raise QFlashLibraryError(f"cannot load {path}: {e}") from e
+        missing = [s for s in EXPORTS if not hasattr(L, s)]
+        if missing:
+            raise QFlashLibraryError(f"{path} lacks exports {missing}")
+        _declare(L)
+        _lib = L
+        return L
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().qflash_hip_last_error().decode(errors="replace")
+        cls = QFlashCompilationError if rc == E_HEADDIM else QFlashLibraryError
+        raise cls(f"{what} failed ({rc}): {msg}")

@@ -1,0 +1,238 @@
+"""Host side of the integer attention forward: the ``qflash`` op namespace.
+
+Mirrors EfficientCompLab/qflash ``qflash/kernel.py`` for this hot path:
+
+* ``qflash_forward`` follows kernel.py:275-351 step for step (asserts, scale,
+  per-tensor absmax scales with the one ``.item()`` sync, fixed-point
+  constants in Python double arithmetic, torch quantisation, mask -> int32
+  bias, launch on torch's current stream, ``o * o_scale``), and raises the
+  same exceptions;
+* ``qflash_kernel`` / ``qflash_masked_kernel`` are launchers with the
+  reference's launch signature (kernel.py:319-326, :339-346) that call the
+  gfx950 HIP kernels through the C ABI (include/qflash_hip.h);
+* ``class qflash`` is the namespace of kernel.py:354-356.
+
+There is no CPU fallback: inputs must live on a GPU and the HIP library
+must be built, otherwise an exception is raised.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import statistics
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+# kernel.py:30-36 - read once at import, like the reference.
+AUTOTUNE_SETTING = os.environ.get("QFLASH_AUTOTUNE", "default")
+USE_CUDA_GRAPH = os.environ.get("QFLASH_CUDA_GRAPH", "0") == "1"
+EXP_USE_SHIFT = os.environ.get("QFLASH_EXP_USE_SHIFT", "1") == "1"
+L_USE_SHIFT = os.environ.get("QFLASH_L_USE_SHIFT", "1") == "1"
+ACC_USE_SHIFT = os.environ.get("QFLASH_ACC_USE_SHIFT", "1") == "1"
+L_SHIFT = int(os.environ.get("QFLASH_L_SHIFT", "30"))
+ACC_SHIFT = int(os.environ.get("QFLASH_ACC_SHIFT", "30"))
+
+LOG2E = 1.44269504      # kernel.py:287 (the literal)
+NEG_INF = -(1 << 20)    # kernel.py:288
+SHIFT = 16              # kernel.py:301
+INT8_MAX = torch.iinfo(torch.int8).max
+_I32 = (-(1 << 31), (1 << 31) - 1)
+
+
+def fixed_point_constants(sm_scale: float, l_shift: int = None, acc_shift: int = None):
+    """(sm_rscale, exp_M, req_M, l_M, acc_M) from sm_scale, kernel.py:300-307.
+
+    Python double arithmetic and half-to-even ``round``; raises
+    ZeroDivisionError / ValueError / OverflowError exactly where the reference
+    does (sm_scale == 0, sm_scale > 2, NaN, inf).
+    """
+    l_shift = L_SHIFT if l_shift is None else l_shift
+    acc_shift = ACC_SHIFT if acc_shift is None else acc_shift
+    sm_rscale = int(round(1.0 / sm_scale))
+    exp_M = int(round(-sm_scale * (1 << SHIFT)))
+    req_M = int(round(sm_scale * 127 * (1 << SHIFT)))
+    l_M = int(round((1 << l_shift) / sm_rscale))
+    acc_M = int(round((1 << acc_shift) / sm_rscale))
+    return sm_rscale, exp_M, req_M, l_M, acc_M
+
+
+def quantize(x: Tensor, x_scale: Tensor) -> Tensor:
+    """clamp(round(x / scale), -128, 127) as int8, kernel.py:309-311."""
+    return torch.clamp(torch.round(x / x_scale), -128, 127).to(torch.int8)
+
+
+def mask_to_bias(attn_mask: Tensor, sm_scale: float, Z: int, H: int, N: int, materialize: bool = False) -> Tensor:
+    """Boolean or float mask -> int32 logit bias of shape (Z, H, N, N), kernel.py:327-336.
+
+    The values equal the reference's; by default the result is an expanded
+    view (stride 0 on broadcast dims) instead of a materialised copy, which
+    the kernels read through their strides.
+    """
+    if attn_mask.dtype == torch.bool:
+        bias = torch.zeros(attn_mask.shape, dtype=torch.int32, device=attn_mask.device)
+        bias.masked_fill_(attn_mask.logical_not(), NEG_INF)
+        bias = bias.expand(Z, H, N, N)
+    else:
+        is_masked = attn_mask < -1e2
+        clipped = attn_mask.masked_fill(is_masked, 0.0)
+        quant = (clipped * LOG2E / sm_scale).round().to(torch.int32)
+        bias = quant.masked_fill(is_masked, NEG_INF).expand(Z, H, N, N)
+    return bias.contiguous() if materialize else bias
+
+
+def _check_i32(**consts):
+    for name, val in consts.items():
+        if not (_I32[0] <= val <= _I32[1]):
+            raise _lib.QFlashLibraryError(
+                f"{name}={val} does not fit int32; the gfx950 kernels take int32 constants")
+
+
+def _stream_ptr(t: Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+class _Launcher:
+    """Launch object with the reference's ``kernel[grid](...)`` call form.
+
+    The grid argument is accepted and ignored: the HIP library chooses its
+    own decomposition.  Positional arguments follow kernel.py:319-326
+    (unmasked) or :339-346 (masked).
+    """
+
+    def __init__(self, masked: bool):
+        self.masked = masked
+        self.__name__ = "qflash_masked_kernel" if masked else "qflash_kernel"
+
+    def __getitem__(self, grid):
+        return self
+
+    def __call__(self, *args, N_CTX: int, HEAD_DIM: int, EXP_USE_SHIFT: bool = True, L_USE_SHIFT: bool = True,
+                 ACC_USE_SHIFT: bool = True, L_SHIFT: int = 16, ACC_SHIFT: int = 16, **_ignored):
+        n_t = 5 if self.masked else 4
+        n_s = 20 if self.masked else 16
+        if len(args) != n_t + 7 + n_s:
+            raise TypeError(f"{self.__name__}: expected {n_t + 7 + n_s} positional arguments, got {len(args)}")
+        tensors = args[:n_t]
+        consts = [int(c) for c in args[n_t:n_t + 5]]
+        strides = [int(s) for s in args[n_t + 5:n_t + 5 + n_s]]
+        Z, H = (int(x) for x in args[n_t + 5 + n_s:n_t + 7 + n_s])
+        for t in tensors:
+            if not t.is_cuda:
+                raise ValueError(f"{self.__name__}: all tensors must be on a GPU device (got {t.device})")
+        _check_i32(sm_rscale=consts[0], exp_M=consts[1], req_M=consts[2], l_M=consts[3], acc_M=consts[4])
+        L = _lib.load()
+        fl = _lib.Flags(int(EXP_USE_SHIFT), int(L_USE_SHIFT), int(ACC_USE_SHIFT), int(L_SHIFT), int(ACC_SHIFT))
+        st = (ctypes.c_int64 * n_s)(*strides)
+        stream = _stream_ptr(tensors[0])
+        ptr = [ctypes.c_void_p(t.data_ptr()) for t in tensors]
+        if self.masked:
+            rc = L.qflash_hip_masked_kernel(*ptr, *consts, st, Z, H, int(N_CTX), int(HEAD_DIM), ctypes.byref(fl),
+                                            stream)
+        else:
+            rc = L.qflash_hip_kernel(*ptr, *consts, st, Z, H, int(N_CTX), int(HEAD_DIM), ctypes.byref(fl), stream)
+        _lib.check(rc, self.__name__)
+
+
+qflash_kernel = _Launcher(masked=False)
+qflash_masked_kernel = _Launcher(masked=True)
+
+
+def bench_latency_ms(fn, warmup: float = 10, rep: float = 100, flush_mb: int = 512, device=None) -> float:
+    """Median kernel time in ms, like triton.testing.do_bench(return_mode='median').
+
+    warmup / rep are time budgets in ms; before every timed run a buffer of
+    flush_mb MB is zeroed so the last-level caches (256 MB MALL on MI355X)
+    do not hold the inputs.  Events are recorded on torch's current stream,
+    the stream the kernels are launched on.
+    """
+    dev = device or torch.device("cuda", torch.cuda.current_device())
+    cache = torch.empty(flush_mb * (1 << 20) // 4, dtype=torch.int32, device=dev)
+    fn()
+    torch.cuda.synchronize(dev)
+    s = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+    for i in range(5):
+        cache.zero_()
+        s[i].record()
+        fn()
+        e[i].record()
+    torch.cuda.synchronize(dev)
+    est = max(sum(a.elapsed_time(b) for a, b in zip(s, e)) / 5, 1e-4)
+    n_warmup = max(1, int(warmup / est))
+    n_rep = max(1, int(rep / est))
+    for _ in range(n_warmup):
+        fn()
+    s = [torch.cuda.Event(enable_timing=True) for _ in range(n_rep)]
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(n_rep)]
+    for i in range(n_rep):
+        cache.zero_()
+        s[i].record()
+        fn()
+        e[i].record()
+    torch.cuda.synchronize(dev)
+    return statistics.median(a.elapsed_time(b) for a, b in zip(s, e))
+
+
+def qflash_forward(
+    query: Tensor,
+    key: Tensor,
+    value: Tensor,
+    attn_mask: Tensor | None = None,
+    scale: float | None = None,
+    return_mode: str = 'output',
+):
+    """Integer-only attention, drop-in for qflash.forward (kernel.py:275-351).
+
+    query/key/value: (Z, H, N, D) floating tensors on the GPU, any strides.
+    attn_mask: None, bool (True = keep) or float additive mask broadcastable
+    to (Z, H, N, N).  Returns ``o_int8 * o_scale`` in the input dtype, or the
+    median kernel time in ms for return_mode='latency'.
+    """
+    d_q, d_k, d_v = query.shape[-1], key.shape[-1], value.shape[-1]
+    assert d_q == d_k and d_k == d_v
+    assert d_k in {16, 32, 64, 128, 256}
+
+    if scale is None:
+        scale = 1.0 / (d_q ** 0.5)
+    scale = scale * LOG2E
+
+    q_scale = query.abs().amax() / INT8_MAX
+    k_scale = key.abs().amax() / INT8_MAX
+    o_scale = value.abs().amax() / INT8_MAX
+    sm_scale = scale * (q_scale * k_scale).item()  # the one host sync, kernel.py:297
+    sm_rscale, exp_M, req_M, l_M, acc_M = fixed_point_constants(sm_scale)
+
+    q8, k8, v8 = quantize(query, q_scale), quantize(key, k_scale), quantize(value, o_scale)
+    o = torch.empty_like(v8)
+    Z, H, N = q8.shape[0], q8.shape[1], q8.shape[2]
+    grid = None  # the HIP library sizes its own launch
+    flag_kw = dict(EXP_USE_SHIFT=EXP_USE_SHIFT, L_USE_SHIFT=L_USE_SHIFT, ACC_USE_SHIFT=ACC_USE_SHIFT,
+                   L_SHIFT=L_SHIFT, ACC_SHIFT=ACC_SHIFT)
+
+    if attn_mask is None:
+        def kernel():
+            qflash_kernel[grid](q8, k8, v8, o, sm_rscale, exp_M, req_M, l_M, acc_M,
+                                *q8.stride(), *k8.stride(), *v8.stride(), *o.stride(),
+                                Z, H, N_CTX=N, HEAD_DIM=d_k, **flag_kw)
+    else:
+        bias = mask_to_bias(attn_mask, sm_scale, Z, H, N)
+
+        def kernel():
+            qflash_masked_kernel[grid](q8, k8, v8, o, bias, sm_rscale, exp_M, req_M, l_M, acc_M,
+                                       *q8.stride(), *k8.stride(), *v8.stride(), *o.stride(), *bias.stride(),
+                                       Z, H, N_CTX=N, HEAD_DIM=d_k, **flag_kw)
+
+    if return_mode == 'latency':
+        return bench_latency_ms(kernel, device=query.device)
+    kernel()
+    return o * o_scale
+
+
+class qflash:
+    """Op namespace of the reference (kernel.py:354-356)."""
+
+    kernel = [qflash_kernel, qflash_masked_kernel]
+    forward = qflash_forward

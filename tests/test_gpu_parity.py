@@ -1,0 +1,147 @@
+"""GPU parity: the gfx950 HIP kernels against the reference's own outputs and the oracle.
+
+* golden vectors written by the reference (Triton interpreter) - every case,
+  through the launcher with the reference's launch signature;
+* the five benchmark configurations x seeds against the C oracle, bit-exact;
+* the end-to-end host path (qflash.forward) against the reference's
+  dequantised outputs;
+* the MFMA register layouts the kernels rely on.
+"""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from golden_io import load_cases
+from oracle import oracle_c
+from oracle.qflash_oracle import Consts, Flags
+
+pytestmark = pytest.mark.gpu
+
+CASES = load_cases()
+DEV = "cuda"
+
+
+def _lib():
+    from qflash_amd import _lib as L
+    return L
+
+
+def _launch(q8, k8, v8, o, consts: Consts, flags: Flags, bias=None):
+    from qflash_amd.kernel import qflash_kernel, qflash_masked_kernel
+    Z, H, N, D = q8.shape
+    kw = dict(N_CTX=N, HEAD_DIM=D, EXP_USE_SHIFT=flags.exp_use_shift, L_USE_SHIFT=flags.l_use_shift,
+              ACC_USE_SHIFT=flags.acc_use_shift, L_SHIFT=flags.l_shift, ACC_SHIFT=flags.acc_shift)
+    c = (consts.sm_rscale, consts.exp_M, consts.req_M, consts.l_M, consts.acc_M)
+    st = (*q8.stride(), *k8.stride(), *v8.stride(), *o.stride())
+    if bias is None:
+        qflash_kernel[None](q8, k8, v8, o, *c, *st, Z, H, **kw)
+    else:
+        qflash_masked_kernel[None](q8, k8, v8, o, bias, *c, *st, *bias.stride(), Z, H, **kw)
+
+
+def test_library_loads_and_reports_version():
+    L = _lib().load()
+    assert b"gfx950" in L.qflash_hip_version()
+
+
+def test_mfma_layout():
+    rng = np.random.default_rng(7)
+    A = rng.integers(-128, 128, (32, 32), dtype=np.int8)
+    B = rng.integers(-128, 128, (32, 32), dtype=np.int8)
+    a, b = torch.from_numpy(A).to(DEV), torch.from_numpy(B).to(DEV)
+    c = torch.zeros(32, 32, dtype=torch.int32, device=DEV)
+    L = _lib().load()
+    import ctypes
+    rc = L.qflash_hip_mfma_layout_check(ctypes.c_void_p(a.data_ptr()), ctypes.c_void_p(b.data_ptr()),
+                                        ctypes.c_void_p(c.data_ptr()), None)
+    assert rc == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(c.cpu().numpy(), A.astype(np.int32) @ B.astype(np.int32))
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_golden_codes(name):
+    c = CASES[name]
+    q8 = torch.from_numpy(c["q_i8"]).to(DEV)
+    k8 = torch.from_numpy(c["k_i8"]).to(DEV)
+    v8 = torch.from_numpy(c["v_i8"]).to(DEV)
+    bias = torch.from_numpy(c["bias_i32"]).to(DEV) if c.masked else None
+    o = torch.empty_like(v8)
+    _launch(q8, k8, v8, o, c.consts, c.flags, bias)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(o.cpu().numpy(), c["o_i8"])
+
+
+@pytest.mark.parametrize("name", [n for n in sorted(CASES) if not CASES[n].masked][:12])
+def test_golden_codes_token_major(name):
+    """Same codes when Q/K/V/O are token-major (B, N, H, D) strided views."""
+    c = CASES[name]
+
+    def tm(a):
+        return torch.from_numpy(a).to(DEV).permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+
+    q8, k8, v8 = tm(c["q_i8"]), tm(c["k_i8"]), tm(c["v_i8"])
+    o = torch.empty_like(v8)
+    assert o.stride() == v8.stride()
+    _launch(q8, k8, v8, o, c.consts, c.flags)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(o.cpu().numpy(), c["o_i8"])
+
+
+@pytest.mark.parametrize("name", [n for n in sorted(CASES) if CASES[n].has_fp and not n.startswith("flags_")])
+def test_golden_forward_end_to_end(name):
+    """qflash.forward on the GPU reproduces the reference's dequantised output."""
+    from qflash_amd import qflash
+    c = CASES[name]
+    dt = torch.float16 if "float16" in str(c["in_dtype"]) else torch.float32
+    q = torch.from_numpy(c["q_fp"]).to(DEV, dt)
+    k = torch.from_numpy(c["k_fp"]).to(DEV, dt)
+    v = torch.from_numpy(c["v_fp"]).to(DEV, dt)
+    mask = None
+    if "mask" in c:
+        mask = torch.from_numpy(c["mask"]).to(DEV)
+    scale = None if np.isnan(c["scale_arg"]) else float(c["scale_arg"])
+    out = qflash.forward(q, k, v, attn_mask=mask, scale=scale)
+    torch.cuda.synchronize()
+    ref = c["out_fp"]
+    got = out.cpu().numpy()
+    assert got.dtype == ref.dtype
+    # bit-exact expected; the bar is 1 ulp of the output dtype
+    ulp = np.spacing(np.abs(ref).astype(ref.dtype)).astype(np.float64)
+    assert np.all(np.abs(got.astype(np.float64) - ref.astype(np.float64)) <= ulp), name
+
+
+def _config_case(cfg_name: str, seed: int):
+    from qflash_amd.kernel import LOG2E, fixed_point_constants, mask_to_bias, quantize
+    from qflash_amd.workloads import CONFIGS, make_inputs
+    cfg = CONFIGS[cfg_name]
+    q, k, v, mask = make_inputs(cfg, seed)
+    qs, ks, vs = (x.abs().amax() / 127 for x in (q, k, v))
+    sm_scale = (1.0 / cfg.D ** 0.5) * LOG2E * (qs * ks).item()
+    consts = Consts(*fixed_point_constants(sm_scale, 30, 30))
+    q8, k8, v8 = quantize(q, qs), quantize(k, ks), quantize(v, vs)
+    bias = None if mask is None else mask_to_bias(mask, sm_scale, cfg.Z, cfg.H, cfg.N)
+    return cfg, consts, q8, k8, v8, bias
+
+
+CONFIG_SEEDS = [(c, s) for c in ("cfg1", "cfg2", "cfg3", "cfg4") for s in (0, 1, 2)] + [("cfg5", 0)]
+
+
+@pytest.mark.parametrize("cfg_name,seed", CONFIG_SEEDS)
+def test_config_codes_vs_oracle(cfg_name, seed):
+    cfg, consts, q8, k8, v8, bias = _config_case(cfg_name, seed)
+    print(f"[case] {cfg_name} seed={seed} consts={consts}", flush=True)
+    want = oracle_c.attention_codes(q8, k8, v8, consts, Flags(), bias=bias, threads=min(16, os.cpu_count() or 1))
+    qd, kd, vd = q8.to(DEV), k8.to(DEV), v8.to(DEV)
+    assert qd.stride() == q8.stride()
+    o = torch.empty_like(vd)
+    bd = None if bias is None else bias.to(DEV)
+    _launch(qd, kd, vd, o, consts, Flags(), bd)
+    torch.cuda.synchronize()
+    got = o.cpu().numpy()
+    n_bad = int((got != want).sum())
+    assert n_bad == 0, f"{n_bad} of {got.size} codes differ"
