@@ -1,0 +1,271 @@
+"""Benchmark of the integer attention forward on one MI355X.
+
+One step = one call of the gfx950 kernel over the headline workload (cfg3,
+ViT-B/384 attention: B=64, H=12, N=577, d=64) with int8 Q/K/V already
+resident in HBM.  Prints ONE JSON line:
+
+  value      int8 TOPS = 4*Z*H*N^2*D / (time per call)
+  roofline   the kernel's achieved TOPS (HIP events on its launch stream) vs
+             the int8 dense MFMA peak, plus HBM bytes per launch from
+             rocprofv3 counters when a summary exists under profiles/
+  cpu_baseline  the C oracle (OpenMP) on the host cores, same workload
+  sqnr_db    dequantised output vs fp32 softmax attention of the
+             unquantised inputs
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3]
+       [--all-configs] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "int8 attention TOPS + us/call at ViT-B/384 shape (B64,H12,N577,d64); SQNR dB"
+PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 MFMA, 5.0 POPS
+PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, 8 TB/s
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "traffic_fwd_cfg3.txt")
+
+
+def host_cores() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def prepare(cfg_name: str, seed: int, dev):
+    """int8 operands on the device + what the checks need (host-side quantisation)."""
+    import torch
+
+    from qflash_amd.kernel import LOG2E, fixed_point_constants, mask_to_bias, quantize
+    from qflash_amd.workloads import CONFIGS, make_inputs
+
+    cfg = CONFIGS[cfg_name]
+    q, k, v, mask = make_inputs(cfg, seed)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    qs, ks, vs = (x.abs().amax() / 127 for x in (qd, kd, vd))
+    sm_scale = (1.0 / cfg.D ** 0.5) * LOG2E * (qs * ks).item()
+    consts = fixed_point_constants(sm_scale, 30, 30)
+    q8, k8, v8 = quantize(qd, qs), quantize(kd, ks), quantize(vd, vs)
+    bias = None if mask is None else mask_to_bias(mask.to(dev), sm_scale, cfg.Z, cfg.H, cfg.N, materialize=True)
+    o = torch.empty_like(v8)
+    return dict(cfg=cfg, q=q, k=k, v=v, mask=mask, q8=q8, k8=k8, v8=v8, o=o, bias=bias, consts=consts,
+                o_scale=vs, sm_scale=sm_scale)
+
+
+def make_step(w):
+    from qflash_amd.kernel import qflash_kernel, qflash_masked_kernel
+
+    cfg, q8, k8, v8, o, bias, c = w["cfg"], w["q8"], w["k8"], w["v8"], w["o"], w["bias"], w["consts"]
+    kw = dict(N_CTX=cfg.N, HEAD_DIM=cfg.D, EXP_USE_SHIFT=True, L_USE_SHIFT=True, ACC_USE_SHIFT=True,
+              L_SHIFT=30, ACC_SHIFT=30)
+    st = (*q8.stride(), *k8.stride(), *v8.stride(), *o.stride())
+    if bias is None:
+        def step():
+            qflash_kernel[None](q8, k8, v8, o, *c, *st, cfg.Z, cfg.H, **kw)
+    else:
+        bst = bias.stride()
+
+        def step():
+            qflash_masked_kernel[None](q8, k8, v8, o, bias, *c, *st, *bst, cfg.Z, cfg.H, **kw)
+    return step
+
+
+def time_steps(step, steps: int, warmup: int):
+    """(wall ms per step, mean per-launch event ms, median per-launch event ms)."""
+    import torch
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        step()
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    ev = [a.elapsed_time(b) for a, b in zip(starts, ends)]
+    return wall, sum(ev) / len(ev), statistics.median(ev)
+
+
+def sqnr_db(w, dev) -> float:
+    """SQNR of codes*o_scale vs fp32 softmax(QK^T/sqrt(D) + mask) V, per head chunk."""
+    import torch
+
+    cfg = w["cfg"]
+    out = w["o"].float() * w["o_scale"].float()
+    num = 0.0
+    den = 0.0
+    scale = 1.0 / math.sqrt(cfg.D)
+    step = max(1, (1 << 26) // (cfg.H * cfg.N * cfg.N))
+    for z0 in range(0, cfg.Z, step):
+        z1 = min(cfg.Z, z0 + step)
+        q = w["q"][z0:z1].to(dev, torch.float32)
+        k = w["k"][z0:z1].to(dev, torch.float32)
+        v = w["v"][z0:z1].to(dev, torch.float32).contiguous()
+        s = torch.matmul(q.contiguous(), k.transpose(-1, -2).contiguous()) * scale
+        if w["mask"] is not None:
+            s = s + w["mask"][z0:z1].to(dev)
+        ref = torch.matmul(torch.softmax(s, dim=-1), v)
+        num += float((ref.double() ** 2).sum())
+        den += float(((out[z0:z1].double() - ref.double()) ** 2).sum())
+    return 10.0 * math.log10(num / den)
+
+
+def flushed_us(step) -> float:
+    from qflash_amd.kernel import bench_latency_ms
+
+    return bench_latency_ms(step, warmup=10, rep=100) * 1e3
+
+
+def read_traffic():
+    """HBM bytes per launch from the committed rocprofv3 counter summary, or None."""
+    try:
+        txt = open(TRAFFIC_SUMMARY).read()
+    except OSError:
+        return None
+    m = re.search(r"^hbm_bytes_per_launch:\s*([0-9.eE+]+)", txt, re.M)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(w, threads: int):
+    """C oracle (test infrastructure) on the host cores over the same int8 inputs."""
+    from oracle import oracle_c
+    from oracle.qflash_oracle import Consts, Flags
+
+    cfg = w["cfg"]
+    q8, k8, v8 = w["q8"].cpu(), w["k8"].cpu(), w["v8"].cpu()
+    bias = None if w["bias"] is None else w["bias"].cpu()
+    c = Consts(*w["consts"])
+    zh = cfg.Z * cfg.H
+    # time a first slice, then size the sample to ~10 s of wall time (all heads at most)
+    n0 = max(1, min(zh, 16))
+    t = time.perf_counter()
+    out = oracle_c.attention_codes(q8, k8, v8, c, Flags(), bias=bias, threads=threads, zh_range=(0, n0))
+    dt0 = time.perf_counter() - t
+    n = max(n0, min(zh, int(n0 * 10.0 / max(dt0, 1e-3))))
+    t = time.perf_counter()
+    out = oracle_c.attention_codes(q8, k8, v8, c, Flags(), bias=bias, threads=threads, zh_range=(0, n), out=out)
+    dt = time.perf_counter() - t
+    ops = 4 * n * cfg.N * cfg.N * cfg.D
+    got = w["o"].cpu().numpy().reshape(zh, cfg.N, cfg.D)[:n]
+    same = bool((out.reshape(zh, cfg.N, cfg.D)[:n] == got).all())
+    return {"value": ops / dt / 1e12, "unit": "TOPS", "cores": threads, "kind": "port",
+            "sample": f"{n} of {zh} (z,h) heads of the same {cfg.name} int8 inputs, 1 rep, {dt:.2f} s",
+            "us_per_call_equiv": dt * 1e6 * zh / n, "codes_match_gpu": same}
+
+
+def run_config(name: str, steps: int, warmup: int, dev, seed: int = 0, cpu: bool = False):
+    w = prepare(name, seed, dev)
+    step = make_step(w)
+    wall_ms, ev_mean_ms, ev_med_ms = time_steps(step, steps, warmup)
+    cfg = w["cfg"]
+    res = {"config": name, "workload": cfg.name, "ops": cfg.ops, "ms_per_step": wall_ms,
+           "us_per_call": ev_mean_ms * 1e3, "us_per_call_median": ev_med_ms * 1e3,
+           "us_per_call_flushed": flushed_us(step), "tops": cfg.ops / (wall_ms * 1e-3) / 1e12,
+           "kernel_tops": cfg.ops / (ev_mean_ms * 1e-3) / 1e12, "sqnr_db": sqnr_db(w, dev),
+           "hbm_gbs_algorithmic": cfg.bytes_min / (ev_mean_ms * 1e-3) / 1e9}
+    if cpu:
+        res["cpu_baseline"] = cpu_baseline(w, host_cores())
+    return res
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="cfg3")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--all-configs", action="store_true", help="also time cfg1..cfg5 (per_config field)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--profile", action="store_true",
+                    help="only the timed kernel launches (for rocprofv3 counter runs)")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
+                    help="run 10 plain device copies of MB MiB (HBM counter calibration) and exit")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the attention forward shards over (z, h) with no exchange, see DESIGN.md", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if args.calibrate_copy:
+        n = args.calibrate_copy << 20
+        src = torch.randint(-128, 127, (n,), dtype=torch.int8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": n, "copies": 10}), flush=True)
+        return 0
+    if args.profile:
+        w = prepare(args.config, args.seed, dev)
+        wall, ev, _ = time_steps(make_step(w), args.steps, args.warmup)
+        print(json.dumps({"config": args.config, "steps": args.steps, "us_per_call": ev * 1e3}), flush=True)
+        return 0
+    head = run_config(args.config, args.steps, args.warmup, dev, args.seed, cpu=not args.no_cpu)
+    cfg_ops = head["ops"]
+    traffic = read_traffic() if args.config == "cfg3" else None
+    achieved = head["kernel_tops"]
+    line = {
+        "metric": METRIC,
+        "value": head["tops"],
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": head["workload"], "Z": None, "H": None, "N": None, "D": None,
+                   "seed": args.seed, "layout": "token-major (B,N,H,D) int8, as QAttention produces",
+                   "timed": "kernel only, int8 Q/K/V resident in HBM"},
+        "us_per_call": head["us_per_call"],
+        "us_per_call_flushed": head["us_per_call_flushed"],
+        "sqnr_db": head["sqnr_db"],
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_INT8_TOPS, "traffic": traffic,
+                     "note": "int8 tera-ops/s (2 ops per MAC, 4*Z*H*N^2*D per call) vs 5.0 POPS dense int8",
+                     "ops_per_launch": cfg_ops,
+                     "hbm_gbs_algorithmic": head["hbm_gbs_algorithmic"]},
+        "cpu_baseline": head.get("cpu_baseline"),
+    }
+    from qflash_amd.workloads import CONFIGS
+    c = CONFIGS[args.config]
+    line["config"].update(Z=c.Z, H=c.H, N=c.N, D=c.D)
+    if args.all_configs:
+        per = []
+        for name in CONFIGS:
+            r = head if name == args.config else run_config(name, max(5, args.steps // 5), 3, dev, args.seed)
+            per.append({k: r[k] for k in ("config", "us_per_call", "us_per_call_flushed", "kernel_tops",
+                                          "sqnr_db", "hbm_gbs_algorithmic")})
+        line["per_config"] = per
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

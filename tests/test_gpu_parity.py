@@ -76,6 +76,19 @@ def test_golden_codes(name):
     np.testing.assert_array_equal(o.cpu().numpy(), c["o_i8"])
 
 
+HOOKS = ["QFLASH_HIP_FORCE_GENERAL", "QFLASH_HIP_FORCE_DYNAMIC_BOUND", "QFLASH_HIP_FORCE_WIDE"]
+
+
+@pytest.mark.parametrize("hook", HOOKS)
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_golden_codes_forced_paths(name, hook, monkeypatch):
+    """Every exact fallback on every case: the general kernel (used when the fast
+    path's guards fail), the fast kernel's per-row dynamic bound for the identity
+    rescale, and its 64-bit rescale of all rows."""
+    monkeypatch.setenv(hook, "1")
+    test_golden_codes(name)
+
+
 @pytest.mark.parametrize("name", [n for n in sorted(CASES) if not CASES[n].masked][:12])
 def test_golden_codes_token_major(name):
     """Same codes when Q/K/V/O are token-major (B, N, H, D) strided views."""
@@ -129,6 +142,13 @@ def _config_case(cfg_name: str, seed: int):
 
 
 CONFIG_SEEDS = [(c, s) for c in ("cfg1", "cfg2", "cfg3", "cfg4") for s in (0, 1, 2)] + [("cfg5", 0)]
+
+
+@pytest.mark.parametrize("hook", HOOKS[1:])
+@pytest.mark.parametrize("cfg_name", ["cfg1", "cfg3", "cfg4"])
+def test_config_codes_forced_paths(cfg_name, hook, monkeypatch):
+    monkeypatch.setenv(hook, "1")
+    test_config_codes_vs_oracle(cfg_name, 1)
 
 
 @pytest.mark.parametrize("cfg_name,seed", CONFIG_SEEDS)
