@@ -194,12 +194,14 @@ def main(argv=None):
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--profile", action="store_true",
                     help="only the timed kernel launches (for rocprofv3 counter runs)")
+    ap.add_argument("--shape", default=None, metavar="Z,H,N,D",
+                    help="with --profile: cfg3-distributed inputs of this shape instead of --config")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                     help="run 10 plain device copies of MB MiB (HBM counter calibration) and exit")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the attention forward shards over (z, h) with no exchange, see DESIGN.md", file=sys.stderr)
+              "the forward shards over (z, h) heads with no exchange besides the 3 absmax scales", file=sys.stderr)
         return 2
 
     import torch
@@ -219,6 +221,11 @@ def main(argv=None):
         print(json.dumps({"calibrate_copy_bytes": n, "copies": 10}), flush=True)
         return 0
     if args.profile:
+        if args.shape:
+            from qflash_amd import workloads
+            Z, H, N, D = (int(x) for x in args.shape.split(","))
+            workloads.CONFIGS["shape"] = workloads.Config(f"Z{Z} H{H} N{N} D{D}", Z, H, N, D)
+            args.config = "shape"
         w = prepare(args.config, args.seed, dev)
         wall, ev, _ = time_steps(make_step(w), args.steps, args.warmup)
         print(json.dumps({"config": args.config, "steps": args.steps, "us_per_call": ev * 1e3}), flush=True)

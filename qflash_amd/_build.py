@@ -23,6 +23,8 @@ HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
+    # MFMA results in VGPRs: the kernels post-process every result with VALU ops
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

@@ -36,6 +36,9 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int32_t kNegInf = -(1 << 20);  // kernel.py:137
+#ifndef QF_FAST_WAVES_D64
+#define QF_FAST_WAVES_D64 3
+#endif
 constexpr int kBN = 32;                   // kernel.py:27, one rescale step
 
 struct Args {
@@ -55,7 +58,7 @@ struct Args {
     int32_t x_safe;  // masked: largest |s - m'| the 24-bit exp path accepts
     int32_t eps_abs; // | |eM|*rs - 2^16 |
     int32_t e_acc;   // | rs*acc_M - 2^acc_shift |
-    int32_t force_wide;  // test hook: start in the exact 64-bit rescale mode
+    int32_t force_robust;  // test hook: general arithmetic for every score, alpha and l
     int32_t n_wg;    // workgroups in the grid (XCD-aware order)
 };
 
@@ -311,6 +314,7 @@ __global__ __launch_bounds__(64 * W) void fwd_general(Args a) {
 // which the host proves from N), a register pair at a time, with one
 // 64-bit multiply-add per element.
 __device__ __forceinline__ int32_t mad24(int32_t a, int32_t b, int32_t c) { return __mul24(a, b) + c; }
+__device__ __forceinline__ int32_t max3(int32_t a, int32_t b, int32_t c) { return max(max(a, b), c); }
 
 template <int D>
 struct Stage {  // 64 keys = two rescale steps per LDS buffer
@@ -400,8 +404,244 @@ __device__ __forceinline__ int32_t rescale_fast(int32_t x, int32_t A, int64_t ha
     return (int32_t)__builtin_amdgcn_alignbit((uint32_t)(p >> 32), (uint32_t)p, (uint32_t)sh);
 }
 
+// Value of the other lane-half (lane ^ 32) combined with this lane's: the
+// two results of v_permlane32_swap are {this, other} in some order.
+__device__ __forceinline__ int32_t half_max(int32_t v) {
+    const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+    return max((int32_t)r[0], (int32_t)r[1]);
+}
+__device__ __forceinline__ int32_t half_sum(int32_t v) {
+    const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+    return (int32_t)(r[0] + r[1]);
+}
+__device__ __forceinline__ int32_t half_min(int32_t v) {
+    const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+    return min((int32_t)r[0], (int32_t)r[1]);
+}
+// Keeps the compiler from distributing a per-row constant back into the
+// per-element expressions (it would turn one mad into mul + sub + add).
+__device__ __forceinline__ int32_t opaque(int32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// E(x) for one x <= 0 inside the fast path's range (see the comment above).
+__device__ __forceinline__ int32_t exp2_fast(int32_t x, int32_t eM, int32_t rs) {
+    const int32_t t = mad24(x, eM, 1 << 16);
+    const int32_t q1 = t >> 16;
+    const int32_t av = x + __mul24(q1, rs) + rs;
+    return av >> min((uint32_t)q1, 31u);
+}
+
+// Per-wave state of the fast kernel (S layout for m, l, bnd: lane = query;
+// O layout for acc).
+template <int D>
+struct FastState {
+    static constexpr int DB = D / 32;
+    i32x16 acc[DB];
+    int32_t m, l;
+    float bnd;  // per-row upper bound on max_d |acc| (dynamic identity proof)
+    int wide;   // sticky: an alpha*acc_M left int32 -> every row is rescaled exactly
+};
+
+template <int D, bool MASKED, bool TAIL>
+__device__ __forceinline__ void load_bias(int32_t* bias_v, const Args& a, const int32_t* brow, int kstart,
+                                          int lane) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int key = kstart + crow(v, lane);
+        bias_v[v] = ((!TAIL || key < a.N) && brow) ? brow[(int64_t)key * a.sb[3]] : 0;
+    }
+}
+
+// S^T tile of one step with bias and padding applied (kernel.py:153-156, :250-253);
+// returns the row max over the 32 columns (both lane halves).
+template <int D, bool MASKED, bool TAIL>
+__device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& a, const i32x4* qv,
+                                          const int8_t* lk, const int32_t* bias_v, int kstart, int lane) {
+    using S = Stage<D>;
+    constexpr int DB = D / 32;
+    const int lq = lane & 31, g = lane >> 5;
+    s = i32x16{};
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+        const i32x4 kf = *reinterpret_cast<const i32x4*>(lk + lq * S::RK + db * 32 + g * 16);
+        s = mfma32(kf, qv[db], s);
+    }
+    smin = INT32_MAX;
+    if constexpr (MASKED) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            s[v] = wadd(s[v], bias_v[v]);
+            if (!TAIL || kstart + crow(v, lane) < a.N) smin = min(smin, s[v]);
+        }
+    }
+    if constexpr (TAIL) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+            if (kstart + crow(v, lane) >= a.N) s[v] = kNegInf;
+    }
+    int32_t mx = max3(s[0], s[1], s[2]);
+    mx = max3(mx, s[3], s[4]);
+    mx = max3(mx, s[5], s[6]);
+    mx = max3(mx, s[7], s[8]);
+    mx = max3(mx, s[9], s[10]);
+    mx = max3(mx, s[11], s[12]);
+    mx = max3(mx, s[13], s[14]);
+    mx = max(mx, s[15]);
+    return half_max(mx);
+}
+
+// One 32-key step (qflash/kernel.py:147-174) for the 32 query rows of a wave.
+// Every branch below is wave-uniform and none of them holds an alternative
+// computation of acc (the accumulators keep their registers across steps).
+template <int D, bool MASKED, bool TAIL>
+__device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const i32x4* qv, const int8_t* lk,
+                                          const int8_t* lvt, const int32_t* brow, int kstart, int lane,
+                                          bool wave_fast, int32_t xlim) {
+    using S = Stage<D>;
+    constexpr int DB = D / 32;
+    const int lq = lane & 31, g = lane >> 5;
+    const int32_t rs = a.rs, eM = a.eM, rM = a.rM;
+
+    int32_t bias_v[16];
+    if constexpr (MASKED) load_bias<D, MASKED, TAIL>(bias_v, a, brow, kstart, lane);
+    i32x16 s;
+    int32_t smin;
+    const int32_t mx = scores<D, MASKED, TAIL>(s, smin, a, qv, lk, bias_v, kstart, lane);
+    const int32_t m = st.m;
+    const int32_t mn = max(m, mx);  // kernel.py:158
+    const int32_t dm = wsub(m, mn);
+    const bool first = kstart == 0;
+
+    bool vec_ok = wave_fast;
+    if constexpr (MASKED) {
+        smin = half_min(smin);
+        vec_ok = vec_ok && __all(smin > -(1 << 23) && mn < (1 << 23) && (int64_t)mn - smin <= xlim);
+    }
+    uint32_t pk[4];
+    if (vec_ok) {
+        // kernel.py:159-161 in six ops per score (see the fast-path comment)
+        const int32_t c1 = opaque(wadd(wmul(wsub(0, mn), eM), 1 << 16));
+        const int32_t c3 = opaque(wsub(rs, mn));
+        const int32_t c15 = opaque(1 << 15);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int32_t t = mad24(s[v], eM, c1);
+            const int32_t q1 = t >> 16;
+            const int32_t av = s[v] + __mul24(q1, rs) + c3;
+            const int32_t E = av >> min((uint32_t)q1, 31u);
+            s[v] = mad24(E, rM, c15);  // p = bits 16..23
+        }
+        if constexpr (TAIL) {  // padded key columns: p(NEG_INF - m') exactly, once per row
+            const int32_t ppad = (int32_t)((uint32_t)requant(exp2_i32(wsub(kNegInf, mn), a), a) << 16);
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                if (kstart + crow(v, lane) >= a.N) s[v] = ppad;
+        }
+#pragma unroll
+        for (int w4 = 0; w4 < 4; ++w4) {
+            const uint32_t lo = __builtin_amdgcn_perm((uint32_t)s[4 * w4 + 1], (uint32_t)s[4 * w4], 0x0c0c0602u);
+            const uint32_t hi = __builtin_amdgcn_perm((uint32_t)s[4 * w4 + 3], (uint32_t)s[4 * w4 + 2], 0x0c0c0602u);
+            pk[w4] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+        }
+    } else {  // general exact arithmetic for this step's scores
+#pragma unroll
+        for (int w4 = 0; w4 < 4; ++w4) {
+            uint32_t wv = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int32_t p = requant(exp2_i32(wsub(s[4 * w4 + e], mn), a), a);
+                wv |= ((uint32_t)p & 0xffu) << (8 * e);
+            }
+            pk[w4] = wv;
+        }
+    }
+    // kernel.py:162
+    int32_t lij = __builtin_amdgcn_sdot4((int)pk[0], 0x01010101, 0, false);
+    lij = __builtin_amdgcn_sdot4((int)pk[1], 0x01010101, lij, false);
+    lij = __builtin_amdgcn_sdot4((int)pk[2], 0x01010101, lij, false);
+    lij = __builtin_amdgcn_sdot4((int)pk[3], 0x01010101, lij, false);
+    lij = half_sum(lij);
+
+    // kernel.py:163-165
+    int32_t alpha;
+    if (!first && wave_fast && __all(-dm <= xlim))
+        alpha = exp2_fast(dm, eM, rs);  // in [-1, rs]
+    else
+        alpha = exp2_i32(dm, a);        // in [-1, rs] unless dm*eM overflows
+    // rs*l_M and rs*acc_M < 2^31 (host): alpha in [-rs, rs] keeps both multipliers in int32
+    const bool wide_step = !__all(alpha >= -rs && alpha <= rs);
+    if (!first && wide_step) st.wide = 1;
+    if (!wide_step) {
+        const int64_t pl = (int64_t)st.l * (int64_t)wmul(alpha, a.lM) + (1ll << (a.l_shift - 1));
+        st.l = wadd((int32_t)__builtin_amdgcn_alignbit((uint32_t)(pl >> 32), (uint32_t)pl, (uint32_t)a.l_shift),
+                    lij);
+    } else {
+        st.l = wadd(release(st.l, alpha, a.lM, a.l_shift, 1, rs), lij);
+    }
+    const int64_t A64 = (int64_t)alpha * a.aM;
+    const int32_t A = (int32_t)A64;
+    // high word of A64 once A's sign is extended (zero unless A64 leaves int32)
+    const int32_t Ah = (int32_t)(A64 >> 32) + (int32_t)((uint32_t)A >> 31);
+    const int32_t as = a.acc_shift;
+    if (!first) {  // acc == 0 before the first step: its rescale is 0 for any alpha
+        const bool dyn = !a.id_ok;
+        const bool need = mn != m || (dyn && st.bnd * (float)a.e_acc >= __builtin_ldexpf(0.99f, as - 1));
+        uint32_t chg = __builtin_amdgcn_readfirstlane((uint32_t)__ballot(need));
+        const int wide = __builtin_amdgcn_readfirstlane(st.wide);
+        if (wide) chg = 0xffffffffu;  // the identity proof no longer holds: rescale every row
+        if (dyn && (need || wide))
+            st.bnd = __builtin_fmaf(st.bnd * (fabsf((float)alpha) * (float)a.aM * __builtin_ldexpf(1.f, -as)),
+                                    1.0000010f, 1.f);
+        if (chg) {
+            // register pair v = rows rlo (lanes 0-31) and rlo+4 (lanes 32-63) of the O layout;
+            // the multiplier of row r sits in lane r of the S layout.
+            // acc*A64 + 2^(as-1) mod 2^64 = acc*sext(A) + 2^(as-1) + (acc*Ah << 32)
+            const int64_t ahalf = 1ll << (as - 1);
+            const int addr = g * 16;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int rlo = 8 * (v >> 2) + (v & 3);
+                if (chg & ((1u << rlo) | (1u << (rlo + 4)))) {
+                    const int32_t av = __builtin_amdgcn_ds_bpermute(addr + 4 * rlo, A);
+                    const int32_t ah = wide ? __builtin_amdgcn_ds_bpermute(addr + 4 * rlo, Ah) : 0;
+#pragma unroll
+                    for (int t = 0; t < DB; ++t) {
+                        const int64_t p = (int64_t)st.acc[t][v] * (int64_t)av + ahalf;
+                        uint32_t hi = (uint32_t)(p >> 32);
+                        if (wide) hi += (uint32_t)wmul(st.acc[t][v], ah);
+                        st.acc[t][v] = (int32_t)__builtin_amdgcn_alignbit(hi, (uint32_t)p, (uint32_t)as);
+                    }
+                }
+            }
+        }
+    }
+    if (!a.id_ok) {  // |P.V| <= 128 * sum|p|, and sum|p| <= sum of the bytes read as unsigned
+        uint32_t sa = __builtin_amdgcn_udot4(pk[0], 0x01010101u, 0u, false);
+        sa = __builtin_amdgcn_udot4(pk[1], 0x01010101u, sa, false);
+        sa = __builtin_amdgcn_udot4(pk[2], 0x01010101u, sa, false);
+        sa = __builtin_amdgcn_udot4(pk[3], 0x01010101u, sa, false);
+        sa = (uint32_t)half_sum((int32_t)sa);
+        st.bnd = (st.bnd + 128.f * (float)sa) * 1.0000010f;
+    }
+    // O += P . V (kernel.py:171)
+    const i32x4 pa = i32x4{(int32_t)pk[0], (int32_t)pk[1], (int32_t)pk[2], (int32_t)pk[3]};
+#pragma unroll
+    for (int t = 0; t < DB; ++t) {
+        const i32x4 vf = *reinterpret_cast<const i32x4*>(lvt + (t * 32 + lq) * S::RV + g * 16);
+        st.acc[t] = mfma32(pa, vf, st.acc[t]);
+    }
+    st.m = mn;  // kernel.py:172
+}
+
+// Occupancy target (waves per SIMD) by head dim: the register budget of the
+// O accumulators (D/32 x 16 VGPRs) and the stage prefetch registers.
+template <int D>
+constexpr int fast_waves_per_simd() { return D <= 32 ? 4 : (D == 64 ? QF_FAST_WAVES_D64 : 2); }
+
 template <int D, int W, bool MASKED>
-__global__ __launch_bounds__(64 * W) void fwd_fast(Args a) {
+__global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Args a) {
     using S = Stage<D>;
     constexpr int NT = 64 * W;
     constexpr int DB = D / 32;
@@ -421,7 +661,8 @@ __global__ __launch_bounds__(64 * W) void fwd_fast(Args a) {
     const int8_t* kb = a.k + z * a.sk[0] + h * a.sk[1];
     const int8_t* vb = a.v + z * a.sv[0] + h * a.sv[1];
     int8_t* ob = a.o + z * a.so[0] + h * a.so[1];
-    const int32_t* bb = MASKED ? a.bias + z * a.sb[0] + h * a.sb[1] + (int64_t)qrow * a.sb[2] : nullptr;
+    const int32_t* brow =
+        (MASKED && qrow < a.N) ? a.bias + z * a.sb[0] + h * a.sb[1] + (int64_t)qrow * a.sb[2] : nullptr;
 
     i32x4 qv[DB];
 #pragma unroll
@@ -429,204 +670,81 @@ __global__ __launch_bounds__(64 * W) void fwd_fast(Args a) {
         qv[db] = qrow < a.N ? *reinterpret_cast<const i32x4*>(qb + (int64_t)qrow * a.sq[2] + db * 32 + g * 16)
                             : i32x4{0, 0, 0, 0};
 
-    const int32_t rs = a.rs, eM = a.eM, rM = a.rM;
-    const int32_t as = a.acc_shift;
     // Unmasked: every real key column of this row has |s| <= 128*||q_row||_1, so
-    // |x| = |s - m'| <= X_row; the 24-bit exp path is exact when X_row*|eM| and
-    // the |a| bound stay in range (checked once for the whole wave).
-    bool wave_fast = true;
+    // |x| = |s - m'| <= X_row for the scores and, past the first step, for
+    // m - m'; the 24-bit path is exact when X_row*|eM| and the |a| bound stay in
+    // range (checked once for the whole wave).  Masked: |x| <= x_safe is checked
+    // per step.
+    bool wave_fast = !a.force_robust;
+    int32_t xlim = a.x_safe;
     if constexpr (!MASKED) {
-        int32_t l1 = 0;
+        // sum |q|: bytes offset by 128 (xor 0x80) against 0x80 under v_sad_u8
+        uint32_t l1u = 0;
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
             for (int w4 = 0; w4 < 4; ++w4)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) l1 += abs((int32_t)(int8_t)((uint32_t)qv[db][w4] >> (8 * e)));
-        l1 += __shfl_xor(l1, 32);
+                l1u = __builtin_amdgcn_sad_u8((uint32_t)qv[db][w4] ^ 0x80808080u, 0x80808080u, l1u);
+        const int32_t l1 = half_sum((int32_t)l1u);
         const int64_t smax = 128ll * l1;
         const int64_t X = smax < (1 << 20) ? 2 * smax : (1 << 20) + smax;
         const int64_t lim = (1ll << 31) - (1ll << 17);
-        const bool ok = X * (int64_t)(-(int64_t)eM) <= lim &&
-                        ((X * a.eps_abs + 65535) >> 16) + 2 * (int64_t)rs + 1 < (1 << 22);
-        wave_fast = __all(ok);
+        const bool ok = X * (int64_t)(-(int64_t)a.eM) <= lim &&
+                        ((X * a.eps_abs + 65535) >> 16) + 2 * (int64_t)a.rs + 1 < (1 << 22);
+        wave_fast = wave_fast && __all(ok);
+        xlim = (int32_t)(X < (1 << 30) ? X : (1 << 30));
     }
-    const int64_t ahalf = 1ll << (as - 1);
-    int32_t m = kNegInf, l = 1;
-    i32x16 acc[DB];
+
+    FastState<D> st;
 #pragma unroll
-    for (int t = 0; t < DB; ++t) acc[t] = i32x16{};
-    bool wide = a.force_wide != 0;  // sticky: an alpha outside [-rs, rs] was seen -> exact 64-bit rescale of all rows
-    // Per-row upper bound on max_d |acc| (only needed when the host could not prove the
-    // identity rescale statically): the rescale by alpha = rs is the identity while
-    // bnd * e_acc < 2^(As-1).
-    float bnd = 0.f;
-    const bool dyn = !a.id_ok;
-    const float e_acc = (float)a.e_acc;
-    const float thr = __builtin_ldexpf(1.f, as - 1) * 0.99f;
-    const float inv_as = __builtin_ldexpf(1.f, -as);
+    for (int t = 0; t < DB; ++t) st.acc[t] = i32x16{};
+    st.m = kNegInf;  // kernel.py:138
+    st.l = 1;        // kernel.py:139
+    st.bnd = 0.f;
+    st.wide = 0;
 
     StageRegs<D, NT> pre;
     stage_load<D, NT>(pre, a, kb, vb, 0, tid);
     stage_store<D, NT>(pre, smem, tid);
     __syncthreads();
 
+    // Full 32-key steps run in the loop; a final partial step (N % 32 != 0) runs
+    // after it from the last stage's buffer, which no later store overwrites.
+    const int nfull = a.N >> 5;
     const int nstage = (a.N + S::KEYS - 1) / S::KEYS;
-    for (int st = 0; st < nstage; ++st) {
-        const int8_t* buf = smem + (st & 1) * S::BYTES;
-        if (st + 1 < nstage) stage_load<D, NT>(pre, a, kb, vb, (st + 1) * S::KEYS, tid);
+    for (int stg = 0; stg < nstage; ++stg) {
+        const int8_t* buf = smem + (stg & 1) * S::BYTES;
+        if (stg + 1 < nstage) stage_load<D, NT>(pre, a, kb, vb, (stg + 1) * S::KEYS, tid);
         if (active) {
 #pragma unroll 1
             for (int half = 0; half < 2; ++half) {
-                const int kstart = st * S::KEYS + half * 32;
-                if (kstart >= a.N) break;
-                const int8_t* lk = buf + half * 32 * S::RK;
-                const int8_t* lvt = buf + S::KBYTES + half * 32;
-                const bool tail = kstart + 32 > a.N;
-
-                int32_t bias_v[16];
-                if constexpr (MASKED) {
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) {
-                        const int key = kstart + crow(v, lane);
-                        bias_v[v] = (key < a.N && qrow < a.N) ? bb[(int64_t)key * a.sb[3]] : 0;
-                    }
-                }
-                i32x16 s = {};
-#pragma unroll
-                for (int db = 0; db < DB; ++db) {
-                    const i32x4 kf = *reinterpret_cast<const i32x4*>(lk + lq * S::RK + db * 32 + g * 16);
-                    s = mfma32(kf, qv[db], s);
-                }
-                int32_t mx = INT32_MIN, smin = INT32_MAX;
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    int32_t x = s[v];
-                    if constexpr (MASKED) {
-                        x = wadd(x, bias_v[v]);
-                        smin = min(smin, (tail && kstart + crow(v, lane) >= a.N) ? INT32_MAX : x);
-                    }
-                    if (tail && kstart + crow(v, lane) >= a.N) x = kNegInf;
-                    s[v] = x;
-                    mx = max(mx, x);
-                }
-                mx = max(mx, __shfl_xor(mx, 32));
-                const int32_t mn = max(m, mx);
-
-                bool vec_ok = wave_fast;
-                if constexpr (MASKED) {
-                    smin = min(smin, __shfl_xor(smin, 32));
-                    // |s| < 2^23 for the 24-bit multiplies, |s - m'| <= x_safe
-                    vec_ok = __all(smin > -(1 << 23) && mn < (1 << 23) && (int64_t)mn - smin <= a.x_safe);
-                }
-                uint32_t pk[4];
-                if (vec_ok) {
-                    const int32_t c1 = wadd(wmul(wsub(0, mn), eM), 1 << 16);
-                    const int32_t c3 = wsub(rs, mn);
-                    int32_t y[16];
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) {
-                        const int32_t t = mad24(s[v], eM, c1);
-                        const int32_t q1 = t >> 16;
-                        const int32_t av = s[v] + __mul24(q1, rs) + c3;
-                        const int32_t E = av >> min((uint32_t)q1, 31u);
-                        y[v] = mad24(E, rM, 1 << 15);
-                    }
-                    if (tail) {  // padded key columns: exact p(NEG_INF - m')
-                        const int32_t ppad = (int32_t)((uint32_t)requant(exp2_i32(wsub(kNegInf, mn), a), a) << 16);
-#pragma unroll
-                        for (int v = 0; v < 16; ++v)
-                            if (kstart + crow(v, lane) >= a.N) y[v] = ppad;
-                    }
-#pragma unroll
-                    for (int w4 = 0; w4 < 4; ++w4) {
-                        const uint32_t lo = __builtin_amdgcn_perm((uint32_t)y[4 * w4 + 1], (uint32_t)y[4 * w4],
-                                                                  0x0c0c0602u);
-                        const uint32_t hi = __builtin_amdgcn_perm((uint32_t)y[4 * w4 + 3], (uint32_t)y[4 * w4 + 2],
-                                                                  0x0c0c0602u);
-                        pk[w4] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
-                    }
-                } else {
-#pragma unroll
-                    for (int w4 = 0; w4 < 4; ++w4) {
-                        uint32_t wv = 0;
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const int32_t p = requant(exp2_i32(wsub(s[4 * w4 + e], mn), a), a);
-                            wv |= ((uint32_t)p & 0xffu) << (8 * e);
-                        }
-                        pk[w4] = wv;
-                    }
-                }
-                int32_t lij = __builtin_amdgcn_sdot4((int)pk[0], 0x01010101, 0, false);
-                lij = __builtin_amdgcn_sdot4((int)pk[1], 0x01010101, lij, false);
-                lij = __builtin_amdgcn_sdot4((int)pk[2], 0x01010101, lij, false);
-                lij = __builtin_amdgcn_sdot4((int)pk[3], 0x01010101, lij, false);
-                lij += __shfl_xor(lij, 32);
-
-                const int32_t alpha = exp2_i32(wsub(m, mn), a);
-                l = wadd(release(l, alpha, a.lM, a.l_shift, a.l_mode, rs), lij);
-                if (kstart > 0) {  // acc == 0 before the first step: its rescale is 0 for any alpha
-                    wide = wide || !__all(alpha >= -rs && alpha <= rs);
-                    const bool need = mn != m || (dyn && bnd * e_acc >= thr);
-                    uint32_t chg = (uint32_t)__ballot(need);
-                    if (wide) chg = 0xffffffffu;
-                    if (dyn && (need || wide))
-                        bnd = __builtin_fmaf(bnd * (fabsf((float)alpha) * (float)a.aM * inv_as), 1.0000010f, 1.f);
-                    if (wide) {
-#pragma unroll
-                        for (int v = 0; v < 16; ++v) {
-                            const int32_t av = __shfl(alpha, crow(v, lane));
-#pragma unroll
-                            for (int t = 0; t < DB; ++t)
-                                acc[t][v] = release(acc[t][v], av, a.aM, as, 1, rs);
-                        }
-                    } else if (chg) {
-                        const int32_t A = wmul(alpha, a.aM);  // |alpha| <= rs: fits int32
-#pragma unroll
-                        for (int v = 0; v < 16; ++v) {
-                            const int rlo = 8 * (v >> 2) + (v & 3);
-                            if (chg & ((1u << rlo) | (1u << (rlo + 4)))) {
-                                const int32_t alo = __builtin_amdgcn_readlane(A, rlo);
-                                const int32_t ahi = __builtin_amdgcn_readlane(A, rlo + 4);
-                                const int32_t av = g ? ahi : alo;
-#pragma unroll
-                                for (int t = 0; t < DB; ++t) acc[t][v] = rescale_fast(acc[t][v], av, ahalf, as);
-                            }
-                        }
-                    }
-                }
-                if (dyn) {  // |P.V| <= 128 * sum|p|, and sum|p| <= sum of the bytes read as unsigned
-                    uint32_t sa = __builtin_amdgcn_udot4(pk[0], 0x01010101u, 0u, false);
-                    sa = __builtin_amdgcn_udot4(pk[1], 0x01010101u, sa, false);
-                    sa = __builtin_amdgcn_udot4(pk[2], 0x01010101u, sa, false);
-                    sa = __builtin_amdgcn_udot4(pk[3], 0x01010101u, sa, false);
-                    sa += __shfl_xor(sa, 32);
-                    bnd = (bnd + 128.f * (float)sa) * 1.0000010f;
-                }
-                const i32x4 pa = i32x4{(int32_t)pk[0], (int32_t)pk[1], (int32_t)pk[2], (int32_t)pk[3]};
-#pragma unroll
-                for (int t = 0; t < DB; ++t) {
-                    const i32x4 vf = *reinterpret_cast<const i32x4*>(lvt + (t * 32 + lq) * S::RV + g * 16);
-                    acc[t] = mfma32(pa, vf, acc[t]);
-                }
-                m = mn;
+                const int step = stg * 2 + half;
+                if (step >= nfull) break;
+                fast_step<D, MASKED, false>(st, a, qv, buf + half * 32 * S::RK, buf + S::KBYTES + half * 32, brow,
+                                            step * 32, lane, wave_fast, xlim);
             }
         }
-        if (st + 1 < nstage) stage_store<D, NT>(pre, smem + ((st + 1) & 1) * S::BYTES, tid);
+        if (stg + 1 < nstage) stage_store<D, NT>(pre, smem + ((stg + 1) & 1) * S::BYTES, tid);
         __syncthreads();
     }
     if (!active) return;
+    if (a.N & 31) {
+        const int8_t* buf = smem + ((nstage - 1) & 1) * S::BYTES;
+        const int th = nfull & 1;
+        fast_step<D, MASKED, true>(st, a, qv, buf + th * 32 * S::RK, buf + S::KBYTES + th * 32, brow, nfull * 32,
+                                   lane, wave_fast, xlim);
+    }
+    // kernel.py:176-180
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
         const int row = crow(v, lane);
-        const int32_t lv = __shfl(l, row);
+        const int32_t lv = __shfl(st.l, row);
         const int orow = q0 + row;
         if (orow >= a.N) continue;
         const float lf = (float)lv;
 #pragma unroll
         for (int t = 0; t < DB; ++t) {
-            const int32_t code = cvt_x86(__fdiv_rn((float)acc[t][v], lf));
+            const int32_t code = cvt_x86(__fdiv_rn((float)st.acc[t][v], lf));
             ob[(int64_t)orow * a.so[2] + t * 32 + lq] = (int8_t)code;
         }
     }
@@ -685,14 +803,17 @@ static hipError_t launch_d(const Args& a, int W, bool vec, bool fast, dim3 grid,
 static bool choose_fast(Args& a, int D, bool masked, bool vec) {
     if (D > 128) return false;  // D=256 would spill: the general kernel serves it
     if (!vec || a.so[3] != 1) return false;
-    if (!a.exp_mode || !a.acc_mode) return false;
-    if (a.acc_shift < 1 || a.acc_shift > 30) return false;
+    if (!a.exp_mode || !a.acc_mode || !a.l_mode) return false;
+    if (a.acc_shift < 1 || a.acc_shift > 30 || a.l_shift < 1 || a.l_shift > 30) return false;
+    if ((int64_t)a.rs * a.aM >= (1ll << 31) || (int64_t)a.rs * a.lM >= (1ll << 31)) return false;
     const int64_t rs = a.rs, eM = a.eM, rM = a.rM, aem = -(int64_t)a.eM;
     if (eM > 0 || aem >= (1 << 23) || rs <= 0 || rs >= (1 << 15) || rM >= (1 << 23) || rM <= -(1 << 23)) return false;
     if (aem * rs >= (1 << 17)) return false;
     const int64_t lim = (1ll << 31) - (1ll << 17);
     // a = x + (q+2)*rs lies in (|x|*eps/2^16 + rs, |x|*eps/2^16 + 2*rs], eps = |eM|*rs - 2^16
     const int64_t eps = aem * rs - 65536, eabs = eps < 0 ? -eps : eps;
+    // |rs - 2^16/|eM|| <= 2 keeps E(x) in [-1, rs] for every x <= 0 with no int32 overflow of x*eM
+    if (eabs > 2 * aem) return false;
     a.eps_abs = (int32_t)eabs;
     // masked: the kernel checks |x| <= X per wave and step; unmasked: per wave from ||q||_1
     int64_t X = aem ? lim / aem : (1ll << 22);
@@ -769,11 +890,11 @@ static int forward(const int8_t* Q, const int8_t* K, const int8_t* V, int8_t* O,
     a.eps_abs = 0;
     a.e_acc = 0;
     // Test hooks (environment, read per call): QFLASH_HIP_FORCE_GENERAL selects the
-    // general kernel; QFLASH_HIP_FORCE_DYNAMIC_BOUND / QFLASH_HIP_FORCE_WIDE drive the
+    // general kernel; QFLASH_HIP_FORCE_DYNAMIC_BOUND / QFLASH_HIP_FORCE_ROBUST drive the
     // fast kernel's exact fallbacks on inputs that would not need them.
     const bool fast = choose_fast(a, D, masked, vec) && !getenv_flag("QFLASH_HIP_FORCE_GENERAL");
     if (getenv_flag("QFLASH_HIP_FORCE_DYNAMIC_BOUND")) a.id_ok = 0;
-    a.force_wide = getenv_flag("QFLASH_HIP_FORCE_WIDE") ? 1 : 0;
+    a.force_robust = getenv_flag("QFLASH_HIP_FORCE_ROBUST") ? 1 : 0;
     dim3 grid((unsigned)nwg);
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;

@@ -188,6 +188,33 @@ def main():
     q, k, v = outlier_qkv(g, torch, 1, 2, 70, 32, torch.float32)
     cases.append(run_case(torch, ref, log, "boolmask_sparse_N70_D32", q, k, v, attn_mask=bm2))
 
+    # 5b. l == 0 at the end of a row: equal logits (one-hot q = k) with the scale
+    #     steered so that 4*p(0) + 28*p(pad) = 0; acc/l is then +-inf or NaN and the
+    #     fp32 -> int32 conversion rule decides the codes.
+    D = 32
+    onehot = torch.zeros(1, 1, 4, D)
+    onehot[..., 0] = 1.0
+    qk32 = float((torch.tensor(1.0) / 127) * (torch.tensor(1.0) / 127))
+    scale_l0 = 0.133345 / (1.44269504 * qk32)
+    vz = torch.zeros(1, 1, 4, D)
+    vz[..., 0, :] = torch.linspace(-1, 1, D)
+    vz[..., 1, :] = torch.linspace(1, -1, D) * 0.5
+    vz[..., 2, 3] = 2.0
+    cases.append(run_case(torch, ref, log, "l_zero_cvt_N4_D32", onehot.clone(), onehot.clone(), vz,
+                          scale=scale_l0))
+
+    # 5c. the running sum starts at l = 1 (kernel.py:139, 242): rows that are fully masked
+    #     and carry zero queries see every logit equal to the mask value, so the
+    #     first step's release of l (alpha = E(NEG_INF - m')) is not rounded away
+    #     and an initial l = 0 would shift every code of those rows.
+    q, k, v = (torch.randn(1, 1, 8, 32, generator=g) for _ in range(3))
+    q[:, :, :4] = 0.0
+    v = (4.0 * (torch.arange(32) % 31 + 1)).float().expand(1, 1, 8, 32).clone()
+    v[..., 0, 31] = 127.0
+    bm3 = torch.ones(1, 1, 8, 8, dtype=torch.bool)
+    bm3[:, :, :4] = False
+    cases.append(run_case(torch, ref, log, "masked_rows_l_init_N8_D32", q, k, v, attn_mask=bm3))
+
     # 6. arithmetic-variant flags (kernel.py:30-36), each its own import.
     variants = {
         "expidiv": {"QFLASH_EXP_USE_SHIFT": "0"},

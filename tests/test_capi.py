@@ -1,0 +1,108 @@
+"""The C ABI (include/qflash_hip.h) on the CPU: the built library loads, exports
+every function the header declares, and rejects bad arguments with the
+documented codes before it touches the GPU (no kernel is launched here)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from qflash_amd import _build, _lib
+
+HEADER = os.path.join(_build.ROOT, "include", "qflash_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qflash_hip_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_build.LIB_PATH):
+        pytest.fail(f"{_build.LIB_PATH} is not built (run __graft_entry__.build())")
+    return _lib.load()
+
+
+def test_header_declares_the_entry_points():
+    assert _declared() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+    nm = subprocess.run(["nm", "-D", "--defined-only", _build.LIB_PATH], capture_output=True, text=True,
+                        check=True).stdout
+    exported = set(re.findall(r"\sT\s(\w+)$", nm, flags=re.M))
+    assert set(_declared()) <= exported
+
+
+def test_version_string(lib):
+    assert b"gfx950" in lib.qflash_hip_version()
+
+
+def _call(lib, masked=False, Q=1, D=64, Z=1, H=1, N=32, rs=100, strides=True, flags=None, bias=1):
+    """Call an entry point with fake non-null pointers: only the host-side checks run."""
+    st = (ctypes.c_int64 * 20)(*([0] * 20)) if strides else None
+    p = ctypes.c_void_p(Q) if Q else None
+    fake = ctypes.c_void_p(64)
+    fl = ctypes.byref(flags) if flags is not None else None
+    if masked:
+        b = ctypes.c_void_p(bias) if bias else None
+        return lib.qflash_hip_masked_kernel(p, fake, fake, fake, b, rs, -1, 1, 1, 1, st, Z, H, N, D, fl, None)
+    return lib.qflash_hip_kernel(p, fake, fake, fake, rs, -1, 1, 1, 1, st, Z, H, N, D, fl, None)
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_invalid_arguments_return_codes_and_messages(lib, masked):
+    assert _call(lib, masked, Q=0) == -1
+    assert b"null pointer" in lib.qflash_hip_last_error()
+    assert _call(lib, masked, strides=False) == -1
+    assert _call(lib, masked, Z=0) == -1
+    assert b"bad shape" in lib.qflash_hip_last_error()
+    assert _call(lib, masked, N=-3) == -1
+    assert _call(lib, masked, rs=0) == -1
+    assert b"sm_rscale" in lib.qflash_hip_last_error()
+    assert _call(lib, masked, D=16) == -2
+    assert b"BLOCK_N" in lib.qflash_hip_last_error()
+    assert _call(lib, masked, D=48) == -2
+    bad = _lib.Flags(1, 1, 1, 0, 30)
+    assert _call(lib, masked, flags=bad) == -1
+    assert b"l_shift" in lib.qflash_hip_last_error()
+    bad = _lib.Flags(1, 1, 1, 30, 63)
+    assert _call(lib, masked, flags=bad) == -1
+    assert b"acc_shift" in lib.qflash_hip_last_error()
+
+
+def test_masked_entry_needs_a_bias(lib):
+    assert _call(lib, masked=True, bias=0) == -1
+    assert b"attn_bias" in lib.qflash_hip_last_error()
+
+
+def test_layout_check_rejects_null(lib):
+    assert lib.qflash_hip_mfma_layout_check(None, None, None, None) == -1
+
+
+def test_error_codes_map_to_python_exceptions(lib):
+    _call(lib, D=16)
+    with pytest.raises(_lib.QFlashCompilationError, match="BLOCK_N"):
+        _lib.check(-2, "qflash_kernel")
+    _call(lib, Z=0)
+    with pytest.raises(_lib.QFlashLibraryError, match="bad shape"):
+        _lib.check(-1, "qflash_kernel")
+    _lib.check(0, "ok")
+
+
+def test_header_compiles_as_c_and_cxx(tmp_path):
+    src = tmp_path / "use.c"
+    src.write_text('#include "qflash_hip.h"\nint main(void){qflash_hip_flags f={1,1,1,30,30};'
+                   'return f.l_shift==30 && sizeof(qflash_hip_flags)==20 ? 0 : 1;}\n')
+    inc = os.path.dirname(HEADER)
+    for cc in (["gcc", "-std=c99"], ["g++", "-x", "c++", "-std=c++17"]):
+        exe = tmp_path / ("a_" + cc[0])
+        subprocess.run([*cc, "-Wall", "-Werror", "-I", inc, str(src), "-o", str(exe)], check=True)
+        subprocess.run([str(exe)], check=True)

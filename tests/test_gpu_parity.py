@@ -76,15 +76,16 @@ def test_golden_codes(name):
     np.testing.assert_array_equal(o.cpu().numpy(), c["o_i8"])
 
 
-HOOKS = ["QFLASH_HIP_FORCE_GENERAL", "QFLASH_HIP_FORCE_DYNAMIC_BOUND", "QFLASH_HIP_FORCE_WIDE"]
+HOOKS = ["QFLASH_HIP_FORCE_GENERAL", "QFLASH_HIP_FORCE_DYNAMIC_BOUND", "QFLASH_HIP_FORCE_ROBUST"]
 
 
 @pytest.mark.parametrize("hook", HOOKS)
 @pytest.mark.parametrize("name", sorted(CASES))
 def test_golden_codes_forced_paths(name, hook, monkeypatch):
     """Every exact fallback on every case: the general kernel (used when the fast
-    path's guards fail), the fast kernel's per-row dynamic bound for the identity
-    rescale, and its 64-bit rescale of all rows."""
+    path's constant guards fail), the fast kernel's per-row dynamic bound for the
+    identity rescale, and its robust continuation (general arithmetic, used
+    when a per-wave or per-step guard fails)."""
     monkeypatch.setenv(hook, "1")
     test_golden_codes(name)
 
