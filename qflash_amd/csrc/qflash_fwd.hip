@@ -22,6 +22,7 @@
 //                      col l%32)
 //   (checked at run time by qflash_hip_mfma_layout_check).
 #include <hip/hip_runtime.h>
+#include <atomic>
 #include <stdint.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -495,7 +496,7 @@ __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& 
 // One 32-key step (qflash/kernel.py:147-174) for the 32 query rows of a wave.
 // Every branch below is wave-uniform and none of them holds an alternative
 // computation of acc (the accumulators keep their registers across steps).
-template <int D, bool MASKED, bool TAIL>
+template <int D, bool MASKED, bool TAIL, bool WIDE>
 __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const i32x4* qv, const int8_t* lk,
                                           const int8_t* lvt, const int32_t* brow, int kstart, int lane,
                                           bool wave_fast, int32_t xlim) {
@@ -566,13 +567,22 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
 
     // kernel.py:163-165
     int32_t alpha;
-    if (!first && wave_fast && __all(-dm <= xlim))
-        alpha = exp2_fast(dm, eM, rs);  // in [-1, rs]
-    else
-        alpha = exp2_i32(dm, a);        // in [-1, rs] unless dm*eM overflows
-    // rs*l_M and rs*acc_M < 2^31 (host): alpha in [-rs, rs] keeps both multipliers in int32
-    const bool wide_step = !__all(alpha >= -rs && alpha <= rs);
-    if (!first && wide_step) st.wide = 1;
+    bool wide_step;
+    if constexpr (!WIDE) {
+        // Unmasked fast waves: past the first step m and m' are maxima of real
+        // scores, so |m - m'| <= 2*smax <= X and alpha = E(m - m') is in [-1, rs].
+        // The first step's alpha may be anything, but acc is still 0 then.
+        alpha = first ? exp2_i32(dm, a) : exp2_fast(dm, eM, rs);
+        wide_step = first;
+    } else {
+        if (!first && wave_fast && __all(-dm <= xlim))
+            alpha = exp2_fast(dm, eM, rs);  // in [-1, rs]
+        else
+            alpha = exp2_i32(dm, a);        // in [-1, rs] unless dm*eM overflows
+        // rs*l_M and rs*acc_M < 2^31 (host): alpha in [-rs, rs] keeps both multipliers in int32
+        wide_step = !__all(alpha >= -rs && alpha <= rs);
+        if (!first && wide_step) st.wide = 1;
+    }
     if (!wide_step) {
         const int64_t pl = (int64_t)st.l * (int64_t)wmul(alpha, a.lM) + (1ll << (a.l_shift - 1));
         st.l = wadd((int32_t)__builtin_amdgcn_alignbit((uint32_t)(pl >> 32), (uint32_t)pl, (uint32_t)a.l_shift),
@@ -589,7 +599,8 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
         const bool dyn = !a.id_ok;
         const bool need = mn != m || (dyn && st.bnd * (float)a.e_acc >= __builtin_ldexpf(0.99f, as - 1));
         uint32_t chg = __builtin_amdgcn_readfirstlane((uint32_t)__ballot(need));
-        const int wide = __builtin_amdgcn_readfirstlane(st.wide);
+        int wide = 0;
+        if constexpr (WIDE) wide = __builtin_amdgcn_readfirstlane(st.wide);
         if (wide) chg = 0xffffffffu;  // the identity proof no longer holds: rescale every row
         if (dyn && (need || wide))
             st.bnd = __builtin_fmaf(st.bnd * (fabsf((float)alpha) * (float)a.aM * __builtin_ldexpf(1.f, -as)),
@@ -605,12 +616,14 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
                 const int rlo = 8 * (v >> 2) + (v & 3);
                 if (chg & ((1u << rlo) | (1u << (rlo + 4)))) {
                     const int32_t av = __builtin_amdgcn_ds_bpermute(addr + 4 * rlo, A);
-                    const int32_t ah = wide ? __builtin_amdgcn_ds_bpermute(addr + 4 * rlo, Ah) : 0;
+                    int32_t ah = 0;
+                    if constexpr (WIDE) ah = wide ? __builtin_amdgcn_ds_bpermute(addr + 4 * rlo, Ah) : 0;
 #pragma unroll
                     for (int t = 0; t < DB; ++t) {
                         const int64_t p = (int64_t)st.acc[t][v] * (int64_t)av + ahalf;
                         uint32_t hi = (uint32_t)(p >> 32);
-                        if (wide) hi += (uint32_t)wmul(st.acc[t][v], ah);
+                        if constexpr (WIDE)
+                            if (wide) hi += (uint32_t)wmul(st.acc[t][v], ah);
                         st.acc[t][v] = (int32_t)__builtin_amdgcn_alignbit(hi, (uint32_t)p, (uint32_t)as);
                     }
                 }
@@ -635,6 +648,72 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     st.m = mn;  // kernel.py:172
 }
 
+// The 32 query rows of one wave: K / V^T stages double-buffered in LDS
+// (loaded into registers one stage ahead), full 32-key steps in the loop, a
+// final partial step (N % 32 != 0) after it from the last stage's buffer,
+// which no later store overwrites, then the rows' int8 codes.  Every wave of
+// the workgroup passes the same barriers, active or not.
+template <int D, int W, bool MASKED, bool WIDE>
+__device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t* smem, const int8_t* kb,
+                                          const int8_t* vb, int8_t* ob, const int32_t* brow, int tid, int lane,
+                                          int q0, bool active, bool wave_fast, int32_t xlim) {
+    using S = Stage<D>;
+    constexpr int NT = 64 * W;
+    constexpr int DB = D / 32;
+    const int lq = lane & 31;
+    FastState<D> st;
+#pragma unroll
+    for (int t = 0; t < DB; ++t) st.acc[t] = i32x16{};
+    st.m = kNegInf;  // kernel.py:138
+    st.l = 1;        // kernel.py:139
+    st.bnd = 0.f;
+    st.wide = 0;
+
+    StageRegs<D, NT> pre;
+    stage_load<D, NT>(pre, a, kb, vb, 0, tid);
+    stage_store<D, NT>(pre, smem, tid);
+    __syncthreads();
+
+    const int nfull = a.N >> 5;
+    const int nstage = (a.N + S::KEYS - 1) / S::KEYS;
+    for (int stg = 0; stg < nstage; ++stg) {
+        const int8_t* buf = smem + (stg & 1) * S::BYTES;
+        if (stg + 1 < nstage) stage_load<D, NT>(pre, a, kb, vb, (stg + 1) * S::KEYS, tid);
+        if (active) {
+#pragma unroll 1
+            for (int half = 0; half < 2; ++half) {
+                const int step = stg * 2 + half;
+                if (step >= nfull) break;
+                fast_step<D, MASKED, false, WIDE>(st, a, qv, buf + half * 32 * S::RK, buf + S::KBYTES + half * 32,
+                                                  brow, step * 32, lane, wave_fast, xlim);
+            }
+        }
+        if (stg + 1 < nstage) stage_store<D, NT>(pre, smem + ((stg + 1) & 1) * S::BYTES, tid);
+        __syncthreads();
+    }
+    if (active && (a.N & 31)) {
+        const int8_t* buf = smem + ((nstage - 1) & 1) * S::BYTES;
+        const int th = nfull & 1;
+        fast_step<D, MASKED, true, WIDE>(st, a, qv, buf + th * 32 * S::RK, buf + S::KBYTES + th * 32, brow,
+                                         nfull * 32, lane, wave_fast, xlim);
+    }
+    if (!active) return;
+    // kernel.py:176-180
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int row = crow(v, lane);
+        const int32_t lv = __shfl(st.l, row);
+        const int orow = q0 + row;
+        if (orow >= a.N) continue;
+        const float lf = (float)lv;
+#pragma unroll
+        for (int t = 0; t < DB; ++t) {
+            const int32_t code = cvt_x86(__fdiv_rn((float)st.acc[t][v], lf));
+            ob[(int64_t)orow * a.so[2] + t * 32 + lq] = (int8_t)code;
+        }
+    }
+}
+
 // Occupancy target (waves per SIMD) by head dim: the register budget of the
 // O accumulators (D/32 x 16 VGPRs) and the stage prefetch registers.
 template <int D>
@@ -643,7 +722,6 @@ constexpr int fast_waves_per_simd() { return D <= 32 ? 4 : (D == 64 ? QF_FAST_WA
 template <int D, int W, bool MASKED>
 __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Args a) {
     using S = Stage<D>;
-    constexpr int NT = 64 * W;
     constexpr int DB = D / 32;
     __shared__ __attribute__((aligned(16))) int8_t smem[2 * S::BYTES];
 
@@ -686,8 +764,8 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
             for (int w4 = 0; w4 < 4; ++w4)
                 l1u = __builtin_amdgcn_sad_u8((uint32_t)qv[db][w4] ^ 0x80808080u, 0x80808080u, l1u);
         const int32_t l1 = half_sum((int32_t)l1u);
-        const int64_t smax = 128ll * l1;
-        const int64_t X = smax < (1 << 20) ? 2 * smax : (1 << 20) + smax;
+        // real columns: x = s - m' >= -2*smax (padded columns are evaluated exactly apart)
+        const int64_t X = 2 * 128ll * l1;
         const int64_t lim = (1ll << 31) - (1ll << 17);
         const bool ok = X * (int64_t)(-(int64_t)a.eM) <= lim &&
                         ((X * a.eps_abs + 65535) >> 16) + 2 * (int64_t)a.rs + 1 < (1 << 22);
@@ -695,58 +773,17 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
         xlim = (int32_t)(X < (1 << 30) ? X : (1 << 30));
     }
 
-    FastState<D> st;
-#pragma unroll
-    for (int t = 0; t < DB; ++t) st.acc[t] = i32x16{};
-    st.m = kNegInf;  // kernel.py:138
-    st.l = 1;        // kernel.py:139
-    st.bnd = 0.f;
-    st.wide = 0;
-
-    StageRegs<D, NT> pre;
-    stage_load<D, NT>(pre, a, kb, vb, 0, tid);
-    stage_store<D, NT>(pre, smem, tid);
-    __syncthreads();
-
-    // Full 32-key steps run in the loop; a final partial step (N % 32 != 0) runs
-    // after it from the last stage's buffer, which no later store overwrites.
-    const int nfull = a.N >> 5;
-    const int nstage = (a.N + S::KEYS - 1) / S::KEYS;
-    for (int stg = 0; stg < nstage; ++stg) {
-        const int8_t* buf = smem + (stg & 1) * S::BYTES;
-        if (stg + 1 < nstage) stage_load<D, NT>(pre, a, kb, vb, (stg + 1) * S::KEYS, tid);
-        if (active) {
-#pragma unroll 1
-            for (int half = 0; half < 2; ++half) {
-                const int step = stg * 2 + half;
-                if (step >= nfull) break;
-                fast_step<D, MASKED, false>(st, a, qv, buf + half * 32 * S::RK, buf + S::KBYTES + half * 32, brow,
-                                            step * 32, lane, wave_fast, xlim);
-            }
-        }
-        if (stg + 1 < nstage) stage_store<D, NT>(pre, smem + ((stg + 1) & 1) * S::BYTES, tid);
-        __syncthreads();
-    }
-    if (!active) return;
-    if (a.N & 31) {
-        const int8_t* buf = smem + ((nstage - 1) & 1) * S::BYTES;
-        const int th = nfull & 1;
-        fast_step<D, MASKED, true>(st, a, qv, buf + th * 32 * S::RK, buf + S::KBYTES + th * 32, brow, nfull * 32,
-                                   lane, wave_fast, xlim);
-    }
-    // kernel.py:176-180
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const int row = crow(v, lane);
-        const int32_t lv = __shfl(st.l, row);
-        const int orow = q0 + row;
-        if (orow >= a.N) continue;
-        const float lf = (float)lv;
-#pragma unroll
-        for (int t = 0; t < DB; ++t) {
-            const int32_t code = cvt_x86(__fdiv_rn((float)st.acc[t][v], lf));
-            ob[(int64_t)orow * a.so[2] + t * 32 + lq] = (int8_t)code;
-        }
+    // Unmasked waves whose guard holds run a loop that never meets an alpha
+    // outside [-1, rs] after the first step; the others (and masked waves) run
+    // the loop that also handles it.  Both pass the same barriers, and each
+    // writes its own rows, so the two never merge register state.
+    if constexpr (!MASKED) {
+        if (wave_fast)
+            fast_rows<D, W, false, false>(a, qv, smem, kb, vb, ob, brow, tid, lane, q0, active, wave_fast, xlim);
+        else
+            fast_rows<D, W, false, true>(a, qv, smem, kb, vb, ob, brow, tid, lane, q0, active, wave_fast, xlim);
+    } else {
+        fast_rows<D, W, true, true>(a, qv, smem, kb, vb, ob, brow, tid, lane, q0, active, wave_fast, xlim);
     }
 }
 
@@ -773,13 +810,77 @@ static int fail(int code, const char* fmt, ...) {
     return code;
 }
 
+// ---- occupancy ------------------------------------------------------------
+// The grid is dealt to the CUs in rounds of (workgroups per CU) x (CUs).  When
+// the last round is nearly empty, a lower occupancy that splits the grid into
+// whole rounds finishes sooner: the workgroups per CU (k) minimise
+// ceil(n_wg / (k * CUs)) * k over k in [kmax - 3, kmax], ties to the larger k.
+// A target k below the kernel's natural occupancy is set by padding the
+// workgroup's LDS allocation (dynamic shared memory the kernel does not use).
+
+static int device_attr(hipDeviceAttribute_t attr) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, attr, dev) != hipSuccess) return 0;
+    return v;
+}
+
+static int pick_wg_per_cu(int64_t nwg, int cus, int kmax) {
+    const char* env = getenv("QFLASH_HIP_WG_PER_CU");  // tuning hook
+    if (env && atoi(env) > 0) return atoi(env) < kmax ? atoi(env) : kmax;
+    if (cus <= 0 || kmax <= 1) return kmax;
+    int best = kmax;
+    int64_t best_cost = ((nwg + (int64_t)kmax * cus - 1) / ((int64_t)kmax * cus)) * kmax;
+    for (int k = kmax - 1; k >= 3 && k >= kmax - 3; --k) {
+        const int64_t cost = ((nwg + (int64_t)k * cus - 1) / ((int64_t)k * cus)) * k;
+        if (cost < best_cost) best = k, best_cost = cost;
+    }
+    return best;
+}
+
+// Dynamic LDS bytes that limit `kern` to k workgroups per CU (cached per k).
+template <typename Kern>
+static size_t lds_pad_for(Kern kern, int block, int k, std::atomic<int>* cache) {
+    int c = cache[k].load(std::memory_order_relaxed);
+    if (c >= 0) return (size_t)c;
+    const int lds_cu = device_attr(hipDeviceAttributeMaxSharedMemoryPerMultiprocessor);
+    hipFuncAttributes fa;
+    int pad = 0;
+    if (lds_cu > 0 && hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(kern)) == hipSuccess) {
+        const int want = (lds_cu / k) & ~511;
+        pad = want > (int)fa.sharedSizeBytes ? want - (int)fa.sharedSizeBytes : 0;
+        if (pad > 48 * 1024) pad = 0;
+        int n = 0;
+        if (pad && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(kern), block,
+                                                                 (size_t)pad) != hipSuccess || n != k))
+            pad = 0;
+    }
+    cache[k].store(pad, std::memory_order_relaxed);
+    return (size_t)pad;
+}
+
+template <int D, int W, bool MASKED>
+static hipError_t launch_fast(const Args& a, dim3 grid, hipStream_t st) {
+    static std::atomic<int> kmax_cache{0};
+    static std::atomic<int> pad_cache[9] = {-1, -1, -1, -1, -1, -1, -1, -1, -1};
+    auto kern = fwd_fast<D, W, MASKED>;
+    int kmax = kmax_cache.load(std::memory_order_relaxed);
+    if (kmax <= 0) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&kmax, reinterpret_cast<const void*>(kern), 64 * W, 0) !=
+            hipSuccess)
+            kmax = 1;
+        kmax = kmax < 1 ? 1 : (kmax > 8 ? 8 : kmax);
+        kmax_cache.store(kmax, std::memory_order_relaxed);
+    }
+    const int k = pick_wg_per_cu(a.n_wg, device_attr(hipDeviceAttributeMultiprocessorCount), kmax);
+    const size_t pad = k < kmax ? lds_pad_for(kern, 64 * W, k, pad_cache) : 0;
+    hipLaunchKernelGGL(kern, grid, dim3(64 * W), pad, st, a);
+    return hipGetLastError();
+}
+
 template <int D, int W, bool MASKED>
 static hipError_t launch_dw(const Args& a, bool vec, bool fast, dim3 grid, hipStream_t st) {
     if constexpr (D <= 128) {
-        if (fast) {
-            hipLaunchKernelGGL((fwd_fast<D, W, MASKED>), grid, dim3(64 * W), 0, st, a);
-            return hipGetLastError();
-        }
+        if (fast) return launch_fast<D, W, MASKED>(a, grid, st);
     }
     if (vec)
         hipLaunchKernelGGL((fwd_general<D, W, MASKED, true>), grid, dim3(64 * W), 0, st, a);

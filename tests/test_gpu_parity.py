@@ -166,3 +166,35 @@ def test_config_codes_vs_oracle(cfg_name, seed):
     got = o.cpu().numpy()
     n_bad = int((got != want).sum())
     assert n_bad == 0, f"{n_bad} of {got.size} codes differ"
+
+
+def _adversarial(pattern: str, D: int, N: int, seed: int):
+    g = np.random.default_rng(seed)
+    if pattern == "uniform":
+        q, k, v = (g.integers(-128, 128, (1, 2, N, D), dtype=np.int64) for _ in range(3))
+    else:  # rows of constant +-128 / 127: the largest |q.k| the int8 range allows
+        q = np.where(g.random((1, 2, N, 1)) < 0.5, -128, 127) * np.ones((1, 2, N, D), dtype=np.int64)
+        k = np.where(g.random((1, 2, N, 1)) < 0.5, -128, 127) * np.ones((1, 2, N, D), dtype=np.int64)
+        q[:, :, ::3] = g.integers(-128, 128, q[:, :, ::3].shape)
+        v = g.integers(-128, 128, (1, 2, N, D), dtype=np.int64)
+    return [torch.from_numpy(x.astype(np.int8)) for x in (q, k, v)]
+
+
+@pytest.mark.parametrize("pattern", ["extreme", "uniform"])
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("sm_scale", [600 / 65536, 0.0123, 0.09, 1.0 / 3000])
+def test_adversarial_int8_inputs(pattern, D, sm_scale):
+    """Full-range int8 operands (constant +-128 rows reach |s| = 128*128*D) under
+    several scales: whichever path the guards pick must stay bit-exact."""
+    from qflash_amd.kernel import fixed_point_constants
+    consts = Consts(*fixed_point_constants(sm_scale, 30, 30))
+    N = 97 if D != 64 else 160
+    q8, k8, v8 = _adversarial(pattern, D, N, seed=D + int(sm_scale * 1e6))
+    print(f"[case] {pattern} D={D} sm_scale={sm_scale} consts={consts}", flush=True)
+    want = oracle_c.attention_codes(q8, k8, v8, consts, Flags(), threads=8)
+    qd, kd, vd = q8.to(DEV), k8.to(DEV), v8.to(DEV)
+    o = torch.empty_like(vd)
+    _launch(qd, kd, vd, o, consts, Flags())
+    torch.cuda.synchronize()
+    got = o.cpu().numpy()
+    assert int((got != want).sum()) == 0
