@@ -648,6 +648,56 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     st.m = mn;  // kernel.py:172
 }
 
+// Output codes of the wave's 32 rows (kernel.py:176-180):
+// out = int8(cvt_x86(RN_f32(fp32(acc) / fp32(l)))).
+// The quotient is taken as RN_f32(a * y) in double precision, y = RN_f64(1/b)
+// once per row.  a * y is within 2^-52 (relative) of a/b, while a/b, for
+// 24-bit a and b, is never within 2^-49 of a midpoint between two floats (it
+// cannot be one: that would need a 25-bit odd significand), so rounding the
+// double to float gives exactly the IEEE single division.  For |b| >= 2 the
+// quotient is below 2^30 in magnitude, so v_cvt_i32_f32 truncates exactly as
+// x86 does; a wave with any row of l in {-1, 0, 1} (quotient +-inf, NaN or
+// 2^31: INT_MIN on x86) takes the IEEE division and the x86 conversion.
+// Bytes go out with buffer stores: rows >= N fall beyond the buffer's range
+// ((N-1)*so2 + D bytes from the head's base, so2 >= D checked by the host)
+// and are dropped by the hardware.
+template <int D>
+__device__ __forceinline__ void fast_store(const FastState<D>& st, const Args& a, int8_t* ob, int lane, int q0) {
+    constexpr int DB = D / 32;
+    const int lq = lane & 31, g = lane >> 5;
+    const float b_row = (float)st.l;            // S layout: lane = row
+    const double y_row = 1.0 / (double)b_row;
+    const int32_t y_lo = (int32_t)(uint32_t)__double_as_longlong(y_row);
+    const int32_t y_hi = (int32_t)(uint32_t)((uint64_t)__double_as_longlong(y_row) >> 32);
+    const bool exact = __any(st.l >= -1 && st.l <= 1);
+    const int32_t so2 = (int32_t)a.so[2];
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(ob, 0, (a.N - 1) * so2 + D, 0x00020000);
+    const int32_t voff = (q0 + 4 * g) * so2 + lq;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int row = crow(v, lane);
+        const int32_t soff = (8 * (v >> 2) + (v & 3)) * so2;
+        if (!exact) {
+            const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * row, y_lo);
+            const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * row, y_hi);
+            const double yd = __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+#pragma unroll
+            for (int t = 0; t < DB; ++t) {
+                const float qf = (float)((double)(float)st.acc[t][v] * yd);
+                __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(int32_t)qf, rsrc, voff + t * 32, soff, 0);
+            }
+        } else {
+            const float bf = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * row, __float_as_int(b_row)));
+#pragma unroll
+            for (int t = 0; t < DB; ++t) {
+                const int32_t code = cvt_x86(__fdiv_rn((float)st.acc[t][v], bf));
+                __builtin_amdgcn_raw_buffer_store_b8((uint8_t)code, rsrc, voff + t * 32, soff, 0);
+            }
+        }
+    }
+}
+
 // The 32 query rows of one wave: K / V^T stages double-buffered in LDS
 // (loaded into registers one stage ahead), full 32-key steps in the loop, a
 // final partial step (N % 32 != 0) after it from the last stage's buffer,
@@ -698,20 +748,7 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
                                          nfull * 32, lane, wave_fast, xlim);
     }
     if (!active) return;
-    // kernel.py:176-180
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const int row = crow(v, lane);
-        const int32_t lv = __shfl(st.l, row);
-        const int orow = q0 + row;
-        if (orow >= a.N) continue;
-        const float lf = (float)lv;
-#pragma unroll
-        for (int t = 0; t < DB; ++t) {
-            const int32_t code = cvt_x86(__fdiv_rn((float)st.acc[t][v], lf));
-            ob[(int64_t)orow * a.so[2] + t * 32 + lq] = (int8_t)code;
-        }
-    }
+    fast_store<D>(st, a, ob, lane, q0);
 }
 
 // Occupancy target (waves per SIMD) by head dim: the register budget of the
@@ -904,6 +941,8 @@ static hipError_t launch_d(const Args& a, int W, bool vec, bool fast, dim3 grid,
 static bool choose_fast(Args& a, int D, bool masked, bool vec) {
     if (D > 128) return false;  // D=256 would spill: the general kernel serves it
     if (!vec || a.so[3] != 1) return false;
+    // buffer stores of O: rows >= N must fall past (N-1)*so2 + D, within 32 bits
+    if (a.so[2] < D || (int64_t)(a.N - 1) * a.so[2] + D > INT32_MAX) return false;
     if (!a.exp_mode || !a.acc_mode || !a.l_mode) return false;
     if (a.acc_shift < 1 || a.acc_shift > 30 || a.l_shift < 1 || a.l_shift > 30) return false;
     if ((int64_t)a.rs * a.aM >= (1ll << 31) || (int64_t)a.rs * a.lM >= (1ll << 31)) return false;

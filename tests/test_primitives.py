@@ -189,3 +189,33 @@ def test_identity_bound_holds_on_real_accumulators():
         m = mn
         worst = max(worst, int(np.abs(acc).max()))
     assert worst <= T * ((1 << 19) + 1) * 2
+
+
+def test_division_through_double_reciprocal_is_ieee_single():
+    """fwd_fast's epilogue: RN_f32(fp64(a) * RN_f64(1/fp64(b))) == RN_f32(a / b) for
+    float a = fp32(acc), |b| = |fp32(l)| >= 2 (random int32 pairs, dense small
+    ranges and near-midpoint families)."""
+    rng = np.random.default_rng(11)
+
+    def check(acc, l):
+        a = acc.astype(np.float32)
+        b = l.astype(np.float32)
+        keep = np.abs(b) >= 2
+        a, b = a[keep], b[keep]
+        want = a / b                                         # IEEE single division
+        got = (a.astype(np.float64) * (1.0 / b.astype(np.float64))).astype(np.float32)
+        bad = np.nonzero(got != want)[0]
+        assert bad.size == 0, f"{bad.size} mismatches, e.g. a={a[bad[0]]!r} b={b[bad[0]]!r}"
+        # and truncation of the in-range quotient equals x86 cvt (|q| < 2^30)
+        assert np.all(np.abs(want) < 2 ** 30)
+
+    for _ in range(4):
+        check(rng.integers(-(1 << 31), 1 << 31, 2_000_000), rng.integers(-(1 << 31), 1 << 31, 2_000_000))
+        check(rng.integers(-(1 << 31), 1 << 31, 2_000_000), rng.integers(-4096, 4096, 2_000_000))
+        check(rng.integers(-(1 << 20), 1 << 20, 2_000_000), rng.integers(2, 1 << 16, 2_000_000))
+    a, b = np.meshgrid(np.arange(-3000, 3000), np.arange(2, 700))
+    check(a.ravel(), b.ravel())
+    # quotients close to midpoints: a = b*(2m+1)/2 +- small, large b
+    b = rng.integers(1 << 20, 1 << 24, 1_000_000)
+    m = rng.integers(1, 1 << 7, 1_000_000)
+    check(b * m + b // 2 + rng.integers(-2, 3, 1_000_000), b)
