@@ -38,7 +38,7 @@ typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int32_t kNegInf = -(1 << 20);  // kernel.py:137
 #ifndef QF_FAST_WAVES_D64
-#define QF_FAST_WAVES_D64 3
+#define QF_FAST_WAVES_D64 4
 #endif
 constexpr int kBN = 32;                   // kernel.py:27, one rescale step
 
@@ -317,80 +317,101 @@ __global__ __launch_bounds__(64 * W) void fwd_general(Args a) {
 __device__ __forceinline__ int32_t mad24(int32_t a, int32_t b, int32_t c) { return __mul24(a, b) + c; }
 __device__ __forceinline__ int32_t max3(int32_t a, int32_t b, int32_t c) { return max(max(a, b), c); }
 
+// K / V stages of 64 keys (two rescale steps) per LDS buffer.  Both tiles
+// hold rows of D bytes exactly as in HBM, copied there by buffer loads that
+// write LDS directly (no registers, no VALU), with the 16-byte chunks of each
+// row permuted by an XOR swizzle so that the MFMA operand reads are free of
+// bank conflicts:
+//   K: chunk c of key k sits at position c ^ kswz(k); lanes 0-7 of a
+//      ds_read_b128 read keys 0-7 at one chunk -> 8 distinct 4-bank groups;
+//   V: chunk c of key k sits at position c ^ vswz(k); V^T fragments are read
+//      with ds_read_b64_tr_b8, whose 16-lane groups read 8 keys x 2 halves of a
+//      chunk -> 16 distinct 2-bank groups.
+// Keys past N read as zeros (buffer range check), as the reference's
+// boundary-checked loads of K and V do.
 template <int D>
-struct Stage {  // 64 keys = two rescale steps per LDS buffer
+struct Stage {
     static constexpr int KEYS = 64;
-    static constexpr int RK = D + 16;             // K row stride (bytes)
-    static constexpr int RV = KEYS + 16;          // V^T row stride (bytes)
-    static constexpr int KBYTES = KEYS * RK;
-    static constexpr int BYTES = KBYTES + D * RV;
-    static constexpr int KCH = KEYS * D / 16;     // 16-byte K chunks
-    static constexpr int VBL = (KEYS / 4) * (D / 4);  // 4x4 byte V blocks
+    static constexpr int CPR = D / 16;       // 16-byte chunks per row
+    static constexpr int KBYTES = KEYS * D;  // one tile (K or V)
+    static constexpr int BYTES = 2 * KBYTES;
+    static constexpr int SLOTS = KEYS * CPR;  // 16-byte slots per tile
+    __device__ static int kswz(int k) {
+        return D == 32 ? (k >> 2) & 1 : (D == 64 ? (k >> 1) & 3 : k & 7);
+    }
+    __device__ static int vswz(int k) {
+        return D == 32 ? (k >> 3) & 1
+                       : (D == 64 ? ((k >> 1) & 1) | (((k >> 3) & 1) << 1) : (k & 3) | (((k >> 3) & 1) << 2));
+    }
 };
 
-template <int D, int NT>
-struct StageRegs {
-    static constexpr int NK = (Stage<D>::KCH + NT - 1) / NT;
-    static constexpr int NV = (Stage<D>::VBL + NT - 1) / NT;
-    i32x4 k[NK];
-    uint32_t v[NV][4];
+// Per-lane byte offsets of the MFMA fragments inside a tile (keys 0-31 of it;
+// the second step of the stage adds 32*D).
+//   K (A operand of S^T = K.Q^T): key lq, chunk 2*db + g.
+//   V (B operand of O = P.V, read transposed): ds_read_b64_tr_b8 gives lane j
+//   of a 16-lane group byte (j & 7) of the 8-byte rows addressed by lanes
+//   2b + (j >> 3), b = 0..7.  Lane i = 2b + h of group G therefore addresses
+//   key 8(b>>2) + 4g + (b&3) (+16 for the fragment's second 8 bytes) and the
+//   8-byte unit 4t + 2(G&1) + h of the row, so that lane n + 32g receives
+//   column 32t + n of the 16 keys the P operand's byte order expects
+//   (byte 16g + b' <-> key 8(b'>>2) + 4g + (b'&3)).
+template <int D>
+struct Frag {
+    static constexpr int DB = D / 32;
+    int32_t k[DB], v[DB];
+    __device__ Frag(int lane) {
+        using S = Stage<D>;
+        const int lq = lane & 31, g = lane >> 5;
+        const int i = lane & 15, G = lane >> 4, b = i >> 1, h = i & 1;
+        const int kv = 8 * (b >> 2) + 4 * (G >> 1) + (b & 3);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) k[db] = lq * D + 16 * ((2 * db + g) ^ S::kswz(lq));
+#pragma unroll
+        for (int t = 0; t < DB; ++t) {
+            const int u = 4 * t + 2 * (G & 1) + h;
+            v[t] = kv * D + 16 * ((u >> 1) ^ S::vswz(kv)) + 8 * (u & 1);
+        }
+    }
 };
 
-template <int D, int NT>
-__device__ __forceinline__ void stage_load(StageRegs<D, NT>& r, const Args& a, const int8_t* kb, const int8_t* vb,
-                                           int kstart, int tid) {
+// Direct HBM -> LDS copies of one stage: slot s of a tile (16 bytes at byte
+// 16*s) holds chunk (s % CPR) ^ swz(key) of key s / CPR; wave w of the
+// workgroup fills slots [r*NT + 64w, r*NT + 64w + 64) in round r.
+template <int D, int W>
+struct StageDma {
     using S = Stage<D>;
+    static constexpr int NT = 64 * W;
+    static constexpr int R = (S::SLOTS + NT - 1) / NT;
+    uint32_t vk[R], vv[R];
+    __device__ StageDma(const Args& a, int wave, int lane) {
 #pragma unroll
-    for (int i = 0; i < StageRegs<D, NT>::NK; ++i) {
-        const int idx = tid + i * NT;
-        const int row = idx / (D / 16), c = idx % (D / 16);
-        const int j = kstart + row;
-        const bool ok = idx < S::KCH && j < a.N;
-        r.k[i] = ok ? *reinterpret_cast<const i32x4*>(kb + (int64_t)j * a.sk[2] + c * 16) : i32x4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int i = 0; i < StageRegs<D, NT>::NV; ++i) {
-        const int idx = tid + i * NT;
-        const int kg = idx / (D / 4), dg = idx % (D / 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int j = kstart + 4 * kg + e;
-            const bool ok = idx < S::VBL && j < a.N;
-            r.v[i][e] = ok ? *reinterpret_cast<const uint32_t*>(vb + (int64_t)j * a.sv[2] + dg * 4) : 0u;
+        for (int r = 0; r < R; ++r) {
+            const int slot = r * NT + wave * 64 + lane;
+            const int key = slot / S::CPR, pos = slot % S::CPR;
+            vk[r] = (uint32_t)(key * (int32_t)a.sk[2] + 16 * (pos ^ S::kswz(key)));
+            vv[r] = (uint32_t)(key * (int32_t)a.sv[2] + 16 * (pos ^ S::vswz(key)));
         }
     }
-}
-
-template <int D, int NT>
-__device__ __forceinline__ void stage_store(const StageRegs<D, NT>& r, int8_t* buf, int tid) {
-    using S = Stage<D>;
-    int8_t* lk = buf;
-    int8_t* lvt = buf + S::KBYTES;
+    __device__ void issue(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv, int8_t* buf, int kstart,
+                          const Args& a, int wave) const {
+        const uint32_t sk = (uint32_t)(kstart * (int32_t)a.sk[2]), sv = (uint32_t)(kstart * (int32_t)a.sv[2]);
 #pragma unroll
-    for (int i = 0; i < StageRegs<D, NT>::NK; ++i) {
-        const int idx = tid + i * NT;
-        if (idx < S::KCH) {
-            const int row = idx / (D / 16), c = idx % (D / 16);
-            *reinterpret_cast<i32x4*>(lk + row * S::RK + c * 16) = r.k[i];
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < StageRegs<D, NT>::NV; ++i) {
-        const int idx = tid + i * NT;
-        if (idx < S::VBL) {
-            const int kg = idx / (D / 4), dg = idx % (D / 4);
-            // keys 4kg..4kg+3 of the stage: step kg/8, lane-half (kg%8)&1, byte group ((kg%8)>>1)
-            const int kl = kg & 7;
-            const int off = (kg >> 3) * 32 + (kl & 1) * 16 + (kl >> 1) * 4;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t c = __builtin_amdgcn_perm(
-                    __builtin_amdgcn_perm(r.v[i][3], r.v[i][2], 0x0c0c0400u | (e * 0x0101u)),
-                    __builtin_amdgcn_perm(r.v[i][1], r.v[i][0], 0x0c0c0400u | (e * 0x0101u)), 0x05040100u);
-                *reinterpret_cast<uint32_t*>(lvt + (dg * 4 + e) * S::RV + off) = c;
+        for (int r = 0; r < R; ++r) {
+            if (r * NT + wave * 64 < S::SLOTS) {
+                int8_t* lk = buf + (r * NT + wave * 64) * 16;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)lk, 16, vk[r],
+                                                         sk, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rv, (__attribute__((address_space(3))) void*)(lk + S::KBYTES), 16, vv[r], sv, 0, 0);
             }
         }
     }
+};
+
+// Completion of this wave's LDS copies (vmcnt), then the workgroup barrier.
+__device__ __forceinline__ void stage_sync() {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
 }
 
 // Workgroup id -> (head, query block) so that consecutive blocks of one head
@@ -459,14 +480,13 @@ __device__ __forceinline__ void load_bias(int32_t* bias_v, const Args& a, const 
 // returns the row max over the 32 columns (both lane halves).
 template <int D, bool MASKED, bool TAIL>
 __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& a, const i32x4* qv,
-                                          const int8_t* lk, const int32_t* bias_v, int kstart, int lane) {
-    using S = Stage<D>;
+                                          const int8_t* lk, const Frag<D>& fr, const int32_t* bias_v, int kstart,
+                                          int lane) {
     constexpr int DB = D / 32;
-    const int lq = lane & 31, g = lane >> 5;
     s = i32x16{};
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
-        const i32x4 kf = *reinterpret_cast<const i32x4*>(lk + lq * S::RK + db * 32 + g * 16);
+        const i32x4 kf = *reinterpret_cast<const i32x4*>(lk + fr.k[db]);
         s = mfma32(kf, qv[db], s);
     }
     smin = INT32_MAX;
@@ -498,9 +518,8 @@ __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& 
 // computation of acc (the accumulators keep their registers across steps).
 template <int D, bool MASKED, bool TAIL, bool WIDE>
 __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const i32x4* qv, const int8_t* lk,
-                                          const int8_t* lvt, const int32_t* brow, int kstart, int lane,
-                                          bool wave_fast, int32_t xlim) {
-    using S = Stage<D>;
+                                          const int8_t* lv, const Frag<D>& fr, const int32_t* brow, int kstart,
+                                          int lane, bool wave_fast, int32_t xlim) {
     constexpr int DB = D / 32;
     const int lq = lane & 31, g = lane >> 5;
     const int32_t rs = a.rs, eM = a.eM, rM = a.rM;
@@ -509,7 +528,7 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     if constexpr (MASKED) load_bias<D, MASKED, TAIL>(bias_v, a, brow, kstart, lane);
     i32x16 s;
     int32_t smin;
-    const int32_t mx = scores<D, MASKED, TAIL>(s, smin, a, qv, lk, bias_v, kstart, lane);
+    const int32_t mx = scores<D, MASKED, TAIL>(s, smin, a, qv, lk, fr, bias_v, kstart, lane);
     const int32_t m = st.m;
     const int32_t mn = max(m, mx);  // kernel.py:158
     const int32_t dm = wsub(m, mn);
@@ -642,7 +661,11 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     const i32x4 pa = i32x4{(int32_t)pk[0], (int32_t)pk[1], (int32_t)pk[2], (int32_t)pk[3]};
 #pragma unroll
     for (int t = 0; t < DB; ++t) {
-        const i32x4 vf = *reinterpret_cast<const i32x4*>(lvt + (t * 32 + lq) * S::RV + g * 16);
+        typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+        typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+        const i32x2 v0 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(lv + fr.v[t]));
+        const i32x2 v1 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(lv + 16 * D + fr.v[t]));
+        const i32x4 vf = i32x4{v0.x, v0.y, v1.x, v1.y};
         st.acc[t] = mfma32(pa, vf, st.acc[t]);
     }
     st.m = mn;  // kernel.py:172
@@ -698,19 +721,18 @@ __device__ __forceinline__ void fast_store(const FastState<D>& st, const Args& a
     }
 }
 
-// The 32 query rows of one wave: K / V^T stages double-buffered in LDS
-// (loaded into registers one stage ahead), full 32-key steps in the loop, a
-// final partial step (N % 32 != 0) after it from the last stage's buffer,
-// which no later store overwrites, then the rows' int8 codes.  Every wave of
-// the workgroup passes the same barriers, active or not.
+// The 32 query rows of one wave: K / V stages double-buffered in LDS (the
+// copy of stage s+1 runs while stage s is consumed), full 32-key steps in the
+// loop, a final partial step (N % 32 != 0) after it from the last stage's
+// buffer, which no later copy overwrites, then the rows' int8 codes.  Every
+// wave of the workgroup issues its share of the copies and passes the same
+// barriers, active or not.
 template <int D, int W, bool MASKED, bool WIDE>
 __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t* smem, const int8_t* kb,
-                                          const int8_t* vb, int8_t* ob, const int32_t* brow, int tid, int lane,
+                                          const int8_t* vb, int8_t* ob, const int32_t* brow, int wave, int lane,
                                           int q0, bool active, bool wave_fast, int32_t xlim) {
     using S = Stage<D>;
-    constexpr int NT = 64 * W;
     constexpr int DB = D / 32;
-    const int lq = lane & 31;
     FastState<D> st;
 #pragma unroll
     for (int t = 0; t < DB; ++t) st.acc[t] = i32x16{};
@@ -719,32 +741,36 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
     st.bnd = 0.f;
     st.wide = 0;
 
-    StageRegs<D, NT> pre;
-    stage_load<D, NT>(pre, a, kb, vb, 0, tid);
-    stage_store<D, NT>(pre, smem, tid);
-    __syncthreads();
+    // K / V of this head as buffers ending after row N-1: rows >= N read as 0
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc((void*)kb, 0, (a.N - 1) * (int32_t)a.sk[2] + D, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc((void*)vb, 0, (a.N - 1) * (int32_t)a.sv[2] + D, 0x00020000);
+    const StageDma<D, W> dma(a, wave, lane);
+    const Frag<D> fr(lane);
+    dma.issue(rk, rv, smem, 0, a, wave);
+    stage_sync();
 
     const int nfull = a.N >> 5;
     const int nstage = (a.N + S::KEYS - 1) / S::KEYS;
     for (int stg = 0; stg < nstage; ++stg) {
         const int8_t* buf = smem + (stg & 1) * S::BYTES;
-        if (stg + 1 < nstage) stage_load<D, NT>(pre, a, kb, vb, (stg + 1) * S::KEYS, tid);
+        if (stg + 1 < nstage) dma.issue(rk, rv, smem + ((stg + 1) & 1) * S::BYTES, (stg + 1) * S::KEYS, a, wave);
         if (active) {
 #pragma unroll 1
             for (int half = 0; half < 2; ++half) {
                 const int step = stg * 2 + half;
                 if (step >= nfull) break;
-                fast_step<D, MASKED, false, WIDE>(st, a, qv, buf + half * 32 * S::RK, buf + S::KBYTES + half * 32,
+                fast_step<D, MASKED, false, WIDE>(st, a, qv, buf + half * 32 * D, buf + S::KBYTES + half * 32 * D, fr,
                                                   brow, step * 32, lane, wave_fast, xlim);
             }
         }
-        if (stg + 1 < nstage) stage_store<D, NT>(pre, smem + ((stg + 1) & 1) * S::BYTES, tid);
-        __syncthreads();
+        stage_sync();
     }
     if (active && (a.N & 31)) {
         const int8_t* buf = smem + ((nstage - 1) & 1) * S::BYTES;
         const int th = nfull & 1;
-        fast_step<D, MASKED, true, WIDE>(st, a, qv, buf + th * 32 * S::RK, buf + S::KBYTES + th * 32, brow,
+        fast_step<D, MASKED, true, WIDE>(st, a, qv, buf + th * 32 * D, buf + S::KBYTES + th * 32 * D, fr, brow,
                                          nfull * 32, lane, wave_fast, xlim);
     }
     if (!active) return;
@@ -752,7 +778,7 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
 }
 
 // Occupancy target (waves per SIMD) by head dim: the register budget of the
-// O accumulators (D/32 x 16 VGPRs) and the stage prefetch registers.
+// O accumulators (D/32 x 16 VGPRs) and the score / exp temporaries.
 template <int D>
 constexpr int fast_waves_per_simd() { return D <= 32 ? 4 : (D == 64 ? QF_FAST_WAVES_D64 : 2); }
 
@@ -763,7 +789,7 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
     __shared__ __attribute__((aligned(16))) int8_t smem[2 * S::BYTES];
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int lq = lane & 31, g = lane >> 5;
     const int wg = xcd_order(blockIdx.x, a.n_wg);
     const int zh = wg / a.mblocks, mb = wg % a.mblocks;
@@ -816,11 +842,11 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
     // writes its own rows, so the two never merge register state.
     if constexpr (!MASKED) {
         if (wave_fast)
-            fast_rows<D, W, false, false>(a, qv, smem, kb, vb, ob, brow, tid, lane, q0, active, wave_fast, xlim);
+            fast_rows<D, W, false, false>(a, qv, smem, kb, vb, ob, brow, wave, lane, q0, active, wave_fast, xlim);
         else
-            fast_rows<D, W, false, true>(a, qv, smem, kb, vb, ob, brow, tid, lane, q0, active, wave_fast, xlim);
+            fast_rows<D, W, false, true>(a, qv, smem, kb, vb, ob, brow, wave, lane, q0, active, wave_fast, xlim);
     } else {
-        fast_rows<D, W, true, true>(a, qv, smem, kb, vb, ob, brow, tid, lane, q0, active, wave_fast, xlim);
+        fast_rows<D, W, true, true>(a, qv, smem, kb, vb, ob, brow, wave, lane, q0, active, wave_fast, xlim);
     }
 }
 
@@ -848,12 +874,11 @@ static int fail(int code, const char* fmt, ...) {
 }
 
 // ---- occupancy ------------------------------------------------------------
-// The grid is dealt to the CUs in rounds of (workgroups per CU) x (CUs).  When
-// the last round is nearly empty, a lower occupancy that splits the grid into
-// whole rounds finishes sooner: the workgroups per CU (k) minimise
-// ceil(n_wg / (k * CUs)) * k over k in [kmax - 3, kmax], ties to the larger k.
-// A target k below the kernel's natural occupancy is set by padding the
-// workgroup's LDS allocation (dynamic shared memory the kernel does not use).
+// The fast kernel runs at its natural occupancy (as many workgroups per CU as
+// its registers allow): measured on MI355X, 4 waves per SIMD beat 3 even where
+// 3 would split the grid into whole rounds (cfg3: 142 us vs 198 us).  The
+// tuning hook QFLASH_HIP_WG_PER_CU lowers it by padding the workgroup's LDS
+// allocation (dynamic shared memory the kernel does not use).
 
 static int device_attr(hipDeviceAttribute_t attr) {
     int dev = 0, v = 0;
@@ -861,17 +886,10 @@ static int device_attr(hipDeviceAttribute_t attr) {
     return v;
 }
 
-static int pick_wg_per_cu(int64_t nwg, int cus, int kmax) {
+static int pick_wg_per_cu(int kmax) {
     const char* env = getenv("QFLASH_HIP_WG_PER_CU");  // tuning hook
     if (env && atoi(env) > 0) return atoi(env) < kmax ? atoi(env) : kmax;
-    if (cus <= 0 || kmax <= 1) return kmax;
-    int best = kmax;
-    int64_t best_cost = ((nwg + (int64_t)kmax * cus - 1) / ((int64_t)kmax * cus)) * kmax;
-    for (int k = kmax - 1; k >= 3 && k >= kmax - 3; --k) {
-        const int64_t cost = ((nwg + (int64_t)k * cus - 1) / ((int64_t)k * cus)) * k;
-        if (cost < best_cost) best = k, best_cost = cost;
-    }
-    return best;
+    return kmax;
 }
 
 // Dynamic LDS bytes that limit `kern` to k workgroups per CU (cached per k).
@@ -908,7 +926,7 @@ static hipError_t launch_fast(const Args& a, dim3 grid, hipStream_t st) {
         kmax = kmax < 1 ? 1 : (kmax > 8 ? 8 : kmax);
         kmax_cache.store(kmax, std::memory_order_relaxed);
     }
-    const int k = pick_wg_per_cu(a.n_wg, device_attr(hipDeviceAttributeMultiprocessorCount), kmax);
+    const int k = pick_wg_per_cu(kmax);
     const size_t pad = k < kmax ? lds_pad_for(kern, 64 * W, k, pad_cache) : 0;
     hipLaunchKernelGGL(kern, grid, dim3(64 * W), pad, st, a);
     return hipGetLastError();
@@ -941,8 +959,10 @@ static hipError_t launch_d(const Args& a, int W, bool vec, bool fast, dim3 grid,
 static bool choose_fast(Args& a, int D, bool masked, bool vec) {
     if (D > 128) return false;  // D=256 would spill: the general kernel serves it
     if (!vec || a.so[3] != 1) return false;
-    // buffer stores of O: rows >= N must fall past (N-1)*so2 + D, within 32 bits
-    if (a.so[2] < D || (int64_t)(a.N - 1) * a.so[2] + D > INT32_MAX) return false;
+    // buffer accesses of K, V (loads) and O (stores): rows >= N must fall past
+    // (N-1)*stride + D, and the last stage's offsets (keys < N + 64) fit 31 bits
+    for (int64_t st : {a.sk[2], a.sv[2], a.so[2]})
+        if (st < D || (int64_t)(a.N + 64) * st + D > INT32_MAX) return false;
     if (!a.exp_mode || !a.acc_mode || !a.l_mode) return false;
     if (a.acc_shift < 1 || a.acc_shift > 30 || a.l_shift < 1 || a.l_shift > 30) return false;
     if ((int64_t)a.rs * a.aM >= (1ll << 31) || (int64_t)a.rs * a.lM >= (1ll << 31)) return false;
