@@ -374,6 +374,51 @@ struct Frag {
     }
 };
 
+// V^T fragments of one step (B operands of O = P.V): two ds_read_b64_tr_b8
+// per 32-column block, the second 16 keys (16*D bytes) further.  Written as
+// one asm block with its own lgkmcnt wait: through the builtin, the compiler
+// would also wait for the in-flight copy of the NEXT stage (vmcnt(0)) before
+// every read, as it cannot tell the two LDS buffers apart.
+template <int D>
+__device__ __forceinline__ void read_vt(i32x4* vf, const int8_t* lv, const Frag<D>& fr) {
+    typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+    const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)lv;
+    i32x2 r[2 * (D / 32)];
+    if constexpr (D == 32) {
+        asm volatile(
+            "ds_read_b64_tr_b8 %0, %2\n\t"
+            "ds_read_b64_tr_b8 %1, %2 offset:%c3\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(r[0]), "=&v"(r[1])
+            : "v"(base + fr.v[0]), "i"(16 * D));
+    } else if constexpr (D == 64) {
+        asm volatile(
+            "ds_read_b64_tr_b8 %0, %4\n\t"
+            "ds_read_b64_tr_b8 %1, %4 offset:%c6\n\t"
+            "ds_read_b64_tr_b8 %2, %5\n\t"
+            "ds_read_b64_tr_b8 %3, %5 offset:%c6\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+            : "v"(base + fr.v[0]), "v"(base + fr.v[1]), "i"(16 * D));
+    } else {
+        asm volatile(
+            "ds_read_b64_tr_b8 %0, %8\n\t"
+            "ds_read_b64_tr_b8 %1, %8 offset:%c12\n\t"
+            "ds_read_b64_tr_b8 %2, %9\n\t"
+            "ds_read_b64_tr_b8 %3, %9 offset:%c12\n\t"
+            "ds_read_b64_tr_b8 %4, %10\n\t"
+            "ds_read_b64_tr_b8 %5, %10 offset:%c12\n\t"
+            "ds_read_b64_tr_b8 %6, %11\n\t"
+            "ds_read_b64_tr_b8 %7, %11 offset:%c12\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]),
+              "=&v"(r[7])
+            : "v"(base + fr.v[0]), "v"(base + fr.v[1]), "v"(base + fr.v[2]), "v"(base + fr.v[3]), "i"(16 * D));
+    }
+#pragma unroll
+    for (int t = 0; t < D / 32; ++t) vf[t] = i32x4{r[2 * t].x, r[2 * t].y, r[2 * t + 1].x, r[2 * t + 1].y};
+}
+
 // Direct HBM -> LDS copies of one stage: slot s of a tile (16 bytes at byte
 // 16*s) holds chunk (s % CPR) ^ swz(key) of key s / CPR; wave w of the
 // workgroup fills slots [r*NT + 64w, r*NT + 64w + 64) in round r.
@@ -516,7 +561,7 @@ __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& 
 // One 32-key step (qflash/kernel.py:147-174) for the 32 query rows of a wave.
 // Every branch below is wave-uniform and none of them holds an alternative
 // computation of acc (the accumulators keep their registers across steps).
-template <int D, bool MASKED, bool TAIL, bool WIDE>
+template <int D, bool MASKED, bool TAIL, bool WIDE, bool DYN>
 __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const i32x4* qv, const int8_t* lk,
                                           const int8_t* lv, const Frag<D>& fr, const int32_t* brow, int kstart,
                                           int lane, bool wave_fast, int32_t xlim) {
@@ -615,15 +660,16 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     const int32_t Ah = (int32_t)(A64 >> 32) + (int32_t)((uint32_t)A >> 31);
     const int32_t as = a.acc_shift;
     if (!first) {  // acc == 0 before the first step: its rescale is 0 for any alpha
-        const bool dyn = !a.id_ok;
-        const bool need = mn != m || (dyn && st.bnd * (float)a.e_acc >= __builtin_ldexpf(0.99f, as - 1));
+        bool need = mn != m;
+        if constexpr (DYN) need = need || st.bnd * (float)a.e_acc >= __builtin_ldexpf(0.99f, as - 1);
         uint32_t chg = __builtin_amdgcn_readfirstlane((uint32_t)__ballot(need));
         int wide = 0;
         if constexpr (WIDE) wide = __builtin_amdgcn_readfirstlane(st.wide);
         if (wide) chg = 0xffffffffu;  // the identity proof no longer holds: rescale every row
-        if (dyn && (need || wide))
-            st.bnd = __builtin_fmaf(st.bnd * (fabsf((float)alpha) * (float)a.aM * __builtin_ldexpf(1.f, -as)),
-                                    1.0000010f, 1.f);
+        if constexpr (DYN)
+            if (need || wide)
+                st.bnd = __builtin_fmaf(st.bnd * (fabsf((float)alpha) * (float)a.aM * __builtin_ldexpf(1.f, -as)),
+                                        1.0000010f, 1.f);
         if (chg) {
             // register pair v = rows rlo (lanes 0-31) and rlo+4 (lanes 32-63) of the O layout;
             // the multiplier of row r sits in lane r of the S layout.
@@ -649,7 +695,7 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
             }
         }
     }
-    if (!a.id_ok) {  // |P.V| <= 128 * sum|p|, and sum|p| <= sum of the bytes read as unsigned
+    if constexpr (DYN) {  // |P.V| <= 128 * sum|p|, and sum|p| <= sum of the bytes read as unsigned
         uint32_t sa = __builtin_amdgcn_udot4(pk[0], 0x01010101u, 0u, false);
         sa = __builtin_amdgcn_udot4(pk[1], 0x01010101u, sa, false);
         sa = __builtin_amdgcn_udot4(pk[2], 0x01010101u, sa, false);
@@ -659,15 +705,10 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     }
     // O += P . V (kernel.py:171)
     const i32x4 pa = i32x4{(int32_t)pk[0], (int32_t)pk[1], (int32_t)pk[2], (int32_t)pk[3]};
+    i32x4 vf[DB];
+    read_vt<D>(vf, lv, fr);
 #pragma unroll
-    for (int t = 0; t < DB; ++t) {
-        typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
-        typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
-        const i32x2 v0 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(lv + fr.v[t]));
-        const i32x2 v1 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(lv + 16 * D + fr.v[t]));
-        const i32x4 vf = i32x4{v0.x, v0.y, v1.x, v1.y};
-        st.acc[t] = mfma32(pa, vf, st.acc[t]);
-    }
+    for (int t = 0; t < DB; ++t) st.acc[t] = mfma32(pa, vf[t], st.acc[t]);
     st.m = mn;  // kernel.py:172
 }
 
@@ -727,7 +768,7 @@ __device__ __forceinline__ void fast_store(const FastState<D>& st, const Args& a
 // buffer, which no later copy overwrites, then the rows' int8 codes.  Every
 // wave of the workgroup issues its share of the copies and passes the same
 // barriers, active or not.
-template <int D, int W, bool MASKED, bool WIDE>
+template <int D, int W, bool MASKED, bool WIDE, bool DYN>
 __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t* smem, const int8_t* kb,
                                           const int8_t* vb, int8_t* ob, const int32_t* brow, int wave, int lane,
                                           int q0, bool active, bool wave_fast, int32_t xlim) {
@@ -761,7 +802,7 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
             for (int half = 0; half < 2; ++half) {
                 const int step = stg * 2 + half;
                 if (step >= nfull) break;
-                fast_step<D, MASKED, false, WIDE>(st, a, qv, buf + half * 32 * D, buf + S::KBYTES + half * 32 * D, fr,
+                fast_step<D, MASKED, false, WIDE, DYN>(st, a, qv, buf + half * 32 * D, buf + S::KBYTES + half * 32 * D, fr,
                                                   brow, step * 32, lane, wave_fast, xlim);
             }
         }
@@ -770,7 +811,7 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
     if (active && (a.N & 31)) {
         const int8_t* buf = smem + ((nstage - 1) & 1) * S::BYTES;
         const int th = nfull & 1;
-        fast_step<D, MASKED, true, WIDE>(st, a, qv, buf + th * 32 * D, buf + S::KBYTES + th * 32 * D, fr, brow,
+        fast_step<D, MASKED, true, WIDE, DYN>(st, a, qv, buf + th * 32 * D, buf + S::KBYTES + th * 32 * D, fr, brow,
                                          nfull * 32, lane, wave_fast, xlim);
     }
     if (!active) return;
@@ -782,7 +823,7 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
 template <int D>
 constexpr int fast_waves_per_simd() { return D <= 32 ? 4 : (D == 64 ? QF_FAST_WAVES_D64 : 2); }
 
-template <int D, int W, bool MASKED>
+template <int D, int W, bool MASKED, bool DYN>
 __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Args a) {
     using S = Stage<D>;
     constexpr int DB = D / 32;
@@ -842,11 +883,11 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
     // writes its own rows, so the two never merge register state.
     if constexpr (!MASKED) {
         if (wave_fast)
-            fast_rows<D, W, false, false>(a, qv, smem, kb, vb, ob, brow, wave, lane, q0, active, wave_fast, xlim);
+            fast_rows<D, W, false, false, DYN>(a, qv, smem, kb, vb, ob, brow, wave, lane, q0, active, wave_fast, xlim);
         else
-            fast_rows<D, W, false, true>(a, qv, smem, kb, vb, ob, brow, wave, lane, q0, active, wave_fast, xlim);
+            fast_rows<D, W, false, true, DYN>(a, qv, smem, kb, vb, ob, brow, wave, lane, q0, active, wave_fast, xlim);
     } else {
-        fast_rows<D, W, true, true>(a, qv, smem, kb, vb, ob, brow, wave, lane, q0, active, wave_fast, xlim);
+        fast_rows<D, W, true, true, DYN>(a, qv, smem, kb, vb, ob, brow, wave, lane, q0, active, wave_fast, xlim);
     }
 }
 
@@ -913,11 +954,11 @@ static size_t lds_pad_for(Kern kern, int block, int k, std::atomic<int>* cache) 
     return (size_t)pad;
 }
 
-template <int D, int W, bool MASKED>
+template <int D, int W, bool MASKED, bool DYN>
 static hipError_t launch_fast(const Args& a, dim3 grid, hipStream_t st) {
     static std::atomic<int> kmax_cache{0};
     static std::atomic<int> pad_cache[9] = {-1, -1, -1, -1, -1, -1, -1, -1, -1};
-    auto kern = fwd_fast<D, W, MASKED>;
+    auto kern = fwd_fast<D, W, MASKED, DYN>;
     int kmax = kmax_cache.load(std::memory_order_relaxed);
     if (kmax <= 0) {
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&kmax, reinterpret_cast<const void*>(kern), 64 * W, 0) !=
@@ -935,7 +976,9 @@ static hipError_t launch_fast(const Args& a, dim3 grid, hipStream_t st) {
 template <int D, int W, bool MASKED>
 static hipError_t launch_dw(const Args& a, bool vec, bool fast, dim3 grid, hipStream_t st) {
     if constexpr (D <= 128) {
-        if (fast) return launch_fast<D, W, MASKED>(a, grid, st);
+        // DYN: the identity of the rescale by alpha = rs is proved per row in-kernel
+        if (fast) return a.id_ok ? launch_fast<D, W, MASKED, false>(a, grid, st)
+                                 : launch_fast<D, W, MASKED, true>(a, grid, st);
     }
     if (vec)
         hipLaunchKernelGGL((fwd_general<D, W, MASKED, true>), grid, dim3(64 * W), 0, st, a);
