@@ -329,9 +329,13 @@ __device__ __forceinline__ int32_t max3(int32_t a, int32_t b, int32_t c) { retur
 //      chunk -> 16 distinct 2-bank groups.
 // Keys past N read as zeros (buffer range check), as the reference's
 // boundary-checked loads of K and V do.
+#ifndef QF_STAGE_STEPS
+#define QF_STAGE_STEPS 2
+#endif
 template <int D>
 struct Stage {
-    static constexpr int KEYS = 64;
+    static constexpr int STEPS = QF_STAGE_STEPS;  // 32-key rescale steps per stage
+    static constexpr int KEYS = 32 * STEPS;
     static constexpr int CPR = D / 16;       // 16-byte chunks per row
     static constexpr int KBYTES = KEYS * D;  // one tile (K or V)
     static constexpr int BYTES = 2 * KBYTES;
@@ -561,7 +565,7 @@ __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& 
 // One 32-key step (qflash/kernel.py:147-174) for the 32 query rows of a wave.
 // Every branch below is wave-uniform and none of them holds an alternative
 // computation of acc (the accumulators keep their registers across steps).
-template <int D, bool MASKED, bool TAIL, bool WIDE, bool DYN>
+template <int D, bool MASKED, bool TAIL, bool WIDE, bool DYN, bool FIRST>
 __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const i32x4* qv, const int8_t* lk,
                                           const int8_t* lv, const Frag<D>& fr, const int32_t* brow, int kstart,
                                           int lane, bool wave_fast, int32_t xlim) {
@@ -577,7 +581,7 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     const int32_t m = st.m;
     const int32_t mn = max(m, mx);  // kernel.py:158
     const int32_t dm = wsub(m, mn);
-    const bool first = kstart == 0;
+    constexpr bool first = FIRST;  // kstart == 0
 
     bool vec_ok = wave_fast;
     if constexpr (MASKED) {
@@ -794,25 +798,36 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
 
     const int nfull = a.N >> 5;
     const int nstage = (a.N + S::KEYS - 1) / S::KEYS;
+    // step 0 (m = NEG_INF, acc = 0) apart from the loop: the loop body then
+    // carries no first-step cases
+    if (active && nfull > 0)
+        fast_step<D, MASKED, false, WIDE, DYN, true>(st, a, qv, smem, smem + S::KBYTES, fr, brow, 0, lane, wave_fast,
+                                                     xlim);
     for (int stg = 0; stg < nstage; ++stg) {
         const int8_t* buf = smem + (stg & 1) * S::BYTES;
         if (stg + 1 < nstage) dma.issue(rk, rv, smem + ((stg + 1) & 1) * S::BYTES, (stg + 1) * S::KEYS, a, wave);
         if (active) {
 #pragma unroll 1
-            for (int half = 0; half < 2; ++half) {
-                const int step = stg * 2 + half;
+            for (int half = stg == 0 ? 1 : 0; half < S::STEPS; ++half) {
+                const int step = stg * S::STEPS + half;
                 if (step >= nfull) break;
-                fast_step<D, MASKED, false, WIDE, DYN>(st, a, qv, buf + half * 32 * D, buf + S::KBYTES + half * 32 * D, fr,
-                                                  brow, step * 32, lane, wave_fast, xlim);
+                fast_step<D, MASKED, false, WIDE, DYN, false>(st, a, qv, buf + half * 32 * D,
+                                                              buf + S::KBYTES + half * 32 * D, fr, brow, step * 32,
+                                                              lane, wave_fast, xlim);
             }
         }
         stage_sync();
     }
     if (active && (a.N & 31)) {
         const int8_t* buf = smem + ((nstage - 1) & 1) * S::BYTES;
-        const int th = nfull & 1;
-        fast_step<D, MASKED, true, WIDE, DYN>(st, a, qv, buf + th * 32 * D, buf + S::KBYTES + th * 32 * D, fr, brow,
-                                         nfull * 32, lane, wave_fast, xlim);
+        const int th = nfull % S::STEPS;
+        const int8_t* lk = buf + th * 32 * D;
+        const int8_t* lv = buf + S::KBYTES + th * 32 * D;
+        if (nfull == 0)
+            fast_step<D, MASKED, true, WIDE, DYN, true>(st, a, qv, lk, lv, fr, brow, 0, lane, wave_fast, xlim);
+        else
+            fast_step<D, MASKED, true, WIDE, DYN, false>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane, wave_fast,
+                                                         xlim);
     }
     if (!active) return;
     fast_store<D>(st, a, ob, lane, q0);
@@ -1082,7 +1097,9 @@ static int forward(const int8_t* Q, const int8_t* K, const int8_t* V, int8_t* O,
         vec = (a.sq[i] % 16 == 0) && (a.sk[i] % 16 == 0) && (a.sv[i] % 16 == 0);
 
     const int blocks32 = (N + 31) / 32;
-    const int W = blocks32 >= 4 ? 4 : (blocks32 >= 2 ? 2 : 1);
+    int W = blocks32 >= 4 ? 4 : (blocks32 >= 2 ? 2 : 1);
+    if (const char* ew = getenv("QFLASH_HIP_WAVES_PER_WG"))  // tuning hook: 1, 2 or 4
+        if (atoi(ew) == 1 || atoi(ew) == 2 || atoi(ew) == 4) W = atoi(ew);
     a.mblocks = (blocks32 + W - 1) / W;
     const int64_t nwg = (int64_t)Z * H * a.mblocks;
     if (nwg > INT32_MAX) return fail(QFLASH_HIP_EINVAL, "grid too large");
