@@ -67,6 +67,22 @@ int qflash_hip_masked_kernel(const int8_t* Q, const int8_t* K, const int8_t* V, 
                              int32_t l_M, int32_t acc_M, const int64_t* strides, int32_t Z, int32_t H,
                              int32_t N_CTX, int32_t HEAD_DIM, const qflash_hip_flags* flags, void* stream);
 
+/*
+ * Masked forward with a window-periodic bias: batch index z uses
+ * attn_bias[z % bias_zmod], i.e. attn_bias has logical shape
+ * (bias_zmod, H, N, N) with the 4 bias strides given as for the masked entry.
+ * No counterpart in the reference: it serves QWindowAttention
+ * (qflash/attention.py:58-75), whose (B_, H, N, N) mask is the relative-position
+ * bias plus a shift mask that repeats every nW windows; passing the nW distinct
+ * slices gives the same codes as qflash_hip_masked_kernel on the materialised
+ * bias without reading or building the B_/nW copies.
+ */
+int qflash_hip_window_kernel(const int8_t* Q, const int8_t* K, const int8_t* V, int8_t* Out,
+                             const int32_t* attn_bias, int32_t sm_rscale, int32_t exp_M, int32_t req_M,
+                             int32_t l_M, int32_t acc_M, const int64_t* strides, int32_t Z, int32_t H,
+                             int32_t N_CTX, int32_t HEAD_DIM, int32_t bias_zmod, const qflash_hip_flags* flags,
+                             void* stream);
+
 /* Message for the last failing call on this thread ("" if none). */
 const char* qflash_hip_last_error(void);
 

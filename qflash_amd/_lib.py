@@ -30,7 +30,7 @@ class Flags(ctypes.Structure):
                 ("acc_shift", ctypes.c_int32)]
 
 
-EXPORTS = ("qflash_hip_kernel", "qflash_hip_masked_kernel", "qflash_hip_last_error",
+EXPORTS = ("qflash_hip_kernel", "qflash_hip_masked_kernel", "qflash_hip_window_kernel", "qflash_hip_last_error",
            "qflash_hip_mfma_layout_check", "qflash_hip_version")
 
 E_HEADDIM = -2
@@ -46,6 +46,9 @@ def _declare(L):
     L.qflash_hip_kernel.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i64p, i32, i32, i32, i32, fp, vp]
     L.qflash_hip_masked_kernel.restype = ctypes.c_int
     L.qflash_hip_masked_kernel.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i64p, i32, i32, i32, i32,
+                                           fp, vp]
+    L.qflash_hip_window_kernel.restype = ctypes.c_int
+    L.qflash_hip_window_kernel.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i64p, i32, i32, i32, i32, i32,
                                            fp, vp]
     L.qflash_hip_last_error.restype = ctypes.c_char_p
     L.qflash_hip_last_error.argtypes = []

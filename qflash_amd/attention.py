@@ -19,7 +19,7 @@ from typing import Dict, Iterable, Optional
 import torch
 from torch import nn
 
-from .kernel import qflash
+from .kernel import qflash, qflash_forward_window
 
 try:  # pragma: no cover - timm is absent in the build image
     from timm.layers import to_2tuple, trunc_normal_
@@ -98,12 +98,11 @@ class QWindowAttention(nn.Module):
         B_, N, C = x.shape
         qkv = self.qkv(x).reshape(B_, N, 3, self.num_heads, -1).permute(2, 0, 3, 1, 4)
         q, k, v = qkv.unbind(0)
-        attn_mask = self._get_rel_pos_bias()
-        if mask is not None:  # (nW, N, N) shift mask, 0 / -100
-            num_win = mask.shape[0]
-            mask = mask.view(1, num_win, 1, N, N).expand(B_ // num_win, -1, self.num_heads, -1, -1)
-            attn_mask = attn_mask + mask.reshape(-1, self.num_heads, N, N)
-        x = qflash.forward(q, k, v, attn_mask=attn_mask)
+        # The reference adds the (nW, N, N) shift mask to the (1, H, N, N) bias
+        # as a materialised (B_, H, N, N) tensor; its values repeat every nW
+        # windows, and qflash_forward_window gives the same codes from the nW
+        # distinct slices.
+        x = qflash_forward_window(q, k, v, self._get_rel_pos_bias(), mask)
         return self.proj(x.transpose(1, 2).reshape(B_, N, -1))
 
     @classmethod

@@ -61,6 +61,8 @@ struct Args {
     int32_t e_acc;   // | rs*acc_M - 2^acc_shift |
     int32_t force_robust;  // test hook: general arithmetic for every score, alpha and l
     int32_t n_wg;    // workgroups in the grid (XCD-aware order)
+    int32_t bias_zmod;  // > 0: the bias of batch index z is bias[z % bias_zmod] (window-periodic)
+    int32_t bias_vec;   // bias rows have unit key stride and non-negative strides: 16-byte buffer loads
 };
 
 // ----------------------------------------------------------------------------
@@ -239,8 +241,8 @@ __global__ __launch_bounds__(64 * W) void fwd_general(Args a) {
             int32_t x = s[v];
             if constexpr (MASKED) {  // kernel.py:250-253
                 if (key < a.N && qrow < a.N)
-                    x = wadd(x, a.bias[z * a.sb[0] + h * a.sb[1] + (int64_t)qrow * a.sb[2] +
-                                       (int64_t)key * a.sb[3]]);
+                    x = wadd(x, a.bias[(a.bias_zmod ? z % a.bias_zmod : z) * a.sb[0] + h * a.sb[1] +
+                                       (int64_t)qrow * a.sb[2] + (int64_t)key * a.sb[3]]);
             }
             if (key >= a.N) x = kNegInf;  // kernel.py:154-156 (never true when N%32==0)
             s[v] = x;
@@ -515,13 +517,32 @@ struct FastState {
     int wide;   // sticky: an alpha*acc_M left int32 -> every row is rescaled exactly
 };
 
-template <int D, bool MASKED, bool TAIL>
-__device__ __forceinline__ void load_bias(int32_t* bias_v, const Args& a, const int32_t* brow, int kstart,
-                                          int lane) {
+// Bias row of one query (kernel.py:232-236, :253) for the masked fast kernel.
+// With unit key stride the 16 values of a lane (keys 8k + 4g + [0, 4) of the
+// step) are four 16-byte buffer loads at lane-constant offsets; keys or rows
+// past the head's bias extent read as 0 (their scores are replaced anyway).
+struct BiasRow {
+    __amdgpu_buffer_rsrc_t rsrc;
+    int32_t voff;        // bytes: (row * sb2 + 4g) * 4
+    const int32_t* row;  // strided fallback (nullptr for rows >= N)
+};
+
+template <bool TAIL>
+__device__ __forceinline__ void load_bias(int32_t* bias_v, const Args& a, const BiasRow& br, int kstart, int lane) {
+    if (a.bias_vec) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const int key = kstart + crow(v, lane);
-        bias_v[v] = ((!TAIL || key < a.N) && brow) ? brow[(int64_t)key * a.sb[3]] : 0;
+        for (int k4 = 0; k4 < 4; ++k4) {
+            const i32x4 b = __builtin_bit_cast(
+                i32x4, __builtin_amdgcn_raw_buffer_load_b128(br.rsrc, br.voff + 32 * k4, 4 * kstart, 0));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bias_v[4 * k4 + e] = b[e];
+        }
+    } else {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int key = kstart + crow(v, lane);
+            bias_v[v] = ((!TAIL || key < a.N) && br.row) ? br.row[(int64_t)key * a.sb[3]] : 0;
+        }
     }
 }
 
@@ -567,14 +588,14 @@ __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& 
 // computation of acc (the accumulators keep their registers across steps).
 template <int D, bool MASKED, bool TAIL, bool WIDE, bool DYN, bool FIRST>
 __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const i32x4* qv, const int8_t* lk,
-                                          const int8_t* lv, const Frag<D>& fr, const int32_t* brow, int kstart,
+                                          const int8_t* lv, const Frag<D>& fr, const BiasRow& brow, int kstart,
                                           int lane, bool wave_fast, int32_t xlim) {
     constexpr int DB = D / 32;
     const int lq = lane & 31, g = lane >> 5;
     const int32_t rs = a.rs, eM = a.eM, rM = a.rM;
 
     int32_t bias_v[16];
-    if constexpr (MASKED) load_bias<D, MASKED, TAIL>(bias_v, a, brow, kstart, lane);
+    if constexpr (MASKED) load_bias<TAIL>(bias_v, a, brow, kstart, lane);
     i32x16 s;
     int32_t smin;
     const int32_t mx = scores<D, MASKED, TAIL>(s, smin, a, qv, lk, fr, bias_v, kstart, lane);
@@ -774,7 +795,7 @@ __device__ __forceinline__ void fast_store(const FastState<D>& st, const Args& a
 // barriers, active or not.
 template <int D, int W, bool MASKED, bool WIDE, bool DYN>
 __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t* smem, const int8_t* kb,
-                                          const int8_t* vb, int8_t* ob, const int32_t* brow, int wave, int lane,
+                                          const int8_t* vb, int8_t* ob, const BiasRow& brow, int wave, int lane,
                                           int q0, bool active, bool wave_fast, int32_t xlim) {
     using S = Stage<D>;
     constexpr int DB = D / 32;
@@ -858,8 +879,19 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
     const int8_t* kb = a.k + z * a.sk[0] + h * a.sk[1];
     const int8_t* vb = a.v + z * a.sv[0] + h * a.sv[1];
     int8_t* ob = a.o + z * a.so[0] + h * a.so[1];
-    const int32_t* brow =
-        (MASKED && qrow < a.N) ? a.bias + z * a.sb[0] + h * a.sb[1] + (int64_t)qrow * a.sb[2] : nullptr;
+    BiasRow brow;
+    if constexpr (MASKED) {
+        const int32_t* bh = a.bias + (a.bias_zmod ? z % a.bias_zmod : z) * a.sb[0] + h * a.sb[1];
+        brow.row = qrow < a.N ? bh + (int64_t)qrow * a.sb[2] : nullptr;
+        // extent of this head's bias: the last element of row N-1 (strides >= 0 when bias_vec)
+        const int32_t nbytes = a.bias_vec ? (int32_t)(((a.N - 1) * a.sb[2] + a.N) * 4) : 0;
+        brow.rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)bh, 0, nbytes, 0x00020000);
+        brow.voff = (int32_t)((qrow * a.sb[2] + 4 * g) * 4);
+    } else {
+        brow.row = nullptr;
+        brow.voff = 0;
+        brow.rsrc = __builtin_amdgcn_make_buffer_rsrc(nullptr, 0, 0, 0x00020000);
+    }
 
     i32x4 qv[DB];
 #pragma unroll
@@ -1059,7 +1091,8 @@ static bool getenv_flag(const char* name) {
 
 static int forward(const int8_t* Q, const int8_t* K, const int8_t* V, int8_t* O, const int32_t* bias,
                    int32_t rs, int32_t eM, int32_t rM, int32_t lM, int32_t aM, const int64_t* strides,
-                   int32_t Z, int32_t H, int32_t N, int32_t D, const qflash_hip_flags* flags, void* stream) {
+                   int32_t Z, int32_t H, int32_t N, int32_t D, const qflash_hip_flags* flags, void* stream,
+                   int32_t bias_zmod = 0) {
     g_err[0] = 0;
     if (!Q || !K || !V || !O || !strides) return fail(QFLASH_HIP_EINVAL, "null pointer argument");
     if (Z <= 0 || H <= 0 || N <= 0) return fail(QFLASH_HIP_EINVAL, "bad shape Z=%d H=%d N=%d", Z, H, N);
@@ -1086,6 +1119,9 @@ static int forward(const int8_t* Q, const int8_t* K, const int8_t* V, int8_t* O,
         a.so[i] = strides[12 + i];
         a.sb[i] = bias ? strides[16 + i] : 0;
     }
+    a.bias_zmod = bias_zmod;
+    a.bias_vec = bias && a.sb[3] == 1 && a.sb[0] >= 0 && a.sb[1] >= 0 && a.sb[2] >= 0 &&
+                 ((int64_t)(N - 1) * a.sb[2] + N + 64) * 4 <= INT32_MAX;
     a.Z = Z; a.H = H; a.N = N;
     a.rs = rs; a.eM = eM; a.rM = rM; a.lM = lM; a.aM = aM;
     a.l_shift = f.l_shift; a.acc_shift = f.acc_shift;
@@ -1154,6 +1190,17 @@ int qflash_hip_masked_kernel(const int8_t* Q, const int8_t* K, const int8_t* V, 
     if (!attn_bias) return qf::fail(QFLASH_HIP_EINVAL, "attn_bias is null");
     return qf::forward(Q, K, V, Out, attn_bias, sm_rscale, exp_M, req_M, l_M, acc_M, strides, Z, H, N_CTX,
                        HEAD_DIM, flags, stream);
+}
+
+int qflash_hip_window_kernel(const int8_t* Q, const int8_t* K, const int8_t* V, int8_t* Out,
+                             const int32_t* attn_bias, int32_t sm_rscale, int32_t exp_M, int32_t req_M,
+                             int32_t l_M, int32_t acc_M, const int64_t* strides, int32_t Z, int32_t H,
+                             int32_t N_CTX, int32_t HEAD_DIM, int32_t bias_zmod, const qflash_hip_flags* flags,
+                             void* stream) {
+    if (!attn_bias) return qf::fail(QFLASH_HIP_EINVAL, "attn_bias is null");
+    if (bias_zmod < 1) return qf::fail(QFLASH_HIP_EINVAL, "bias_zmod must be >= 1 (got %d)", bias_zmod);
+    return qf::forward(Q, K, V, Out, attn_bias, sm_rscale, exp_M, req_M, l_M, acc_M, strides, Z, H, N_CTX,
+                       HEAD_DIM, flags, stream, bias_zmod);
 }
 
 const char* qflash_hip_last_error(void) { return qf::g_err; }

@@ -64,6 +64,22 @@ def quantize(x: Tensor, x_scale: Tensor) -> Tensor:
     return torch.clamp(torch.round(x / x_scale), -128, 127).to(torch.int8)
 
 
+def bias_values(attn_mask: Tensor, sm_scale: float) -> Tensor:
+    """Elementwise mask -> int32 logit bias, same shape as the mask (kernel.py:327-336).
+
+    bool: 0 where True, NEG_INF where False.  float: values < -1e2 are masked
+    (NEG_INF), the others become round(x * LOG2E / sm_scale) in the mask's
+    dtype, as the reference's torch ops compute them.
+    """
+    if attn_mask.dtype == torch.bool:
+        bias = torch.zeros(attn_mask.shape, dtype=torch.int32, device=attn_mask.device)
+        return bias.masked_fill_(attn_mask.logical_not(), NEG_INF)
+    is_masked = attn_mask < -1e2
+    clipped = attn_mask.masked_fill(is_masked, 0.0)
+    quant = (clipped * LOG2E / sm_scale).round().to(torch.int32)
+    return quant.masked_fill(is_masked, NEG_INF)
+
+
 def mask_to_bias(attn_mask: Tensor, sm_scale: float, Z: int, H: int, N: int, materialize: bool = False) -> Tensor:
     """Boolean or float mask -> int32 logit bias of shape (Z, H, N, N), kernel.py:327-336.
 
@@ -71,15 +87,7 @@ def mask_to_bias(attn_mask: Tensor, sm_scale: float, Z: int, H: int, N: int, mat
     view (stride 0 on broadcast dims) instead of a materialised copy, which
     the kernels read through their strides.
     """
-    if attn_mask.dtype == torch.bool:
-        bias = torch.zeros(attn_mask.shape, dtype=torch.int32, device=attn_mask.device)
-        bias.masked_fill_(attn_mask.logical_not(), NEG_INF)
-        bias = bias.expand(Z, H, N, N)
-    else:
-        is_masked = attn_mask < -1e2
-        clipped = attn_mask.masked_fill(is_masked, 0.0)
-        quant = (clipped * LOG2E / sm_scale).round().to(torch.int32)
-        bias = quant.masked_fill(is_masked, NEG_INF).expand(Z, H, N, N)
+    bias = bias_values(attn_mask, sm_scale).expand(Z, H, N, N)
     return bias.contiguous() if materialize else bias
 
 
@@ -138,6 +146,33 @@ class _Launcher:
 
 qflash_kernel = _Launcher(masked=False)
 qflash_masked_kernel = _Launcher(masked=True)
+
+
+def qflash_window_kernel(q8: Tensor, k8: Tensor, v8: Tensor, o: Tensor, bias: Tensor, consts, bias_zmod: int,
+                         flags: dict) -> None:
+    """Masked launch with a window-periodic bias (include/qflash_hip.h: qflash_hip_window_kernel).
+
+    bias has shape (bias_zmod, H, N, N); batch index z of Q/K/V/O uses
+    bias[z % bias_zmod].  No counterpart in the reference: QWindowAttention's
+    (B_, H, N, N) mask repeats every nW windows, and this launch reads the nW
+    distinct slices instead of a materialised copy.
+    """
+    Z, H, N, D = q8.shape
+    for t in (q8, k8, v8, o, bias):
+        if not t.is_cuda:
+            raise ValueError(f"qflash_window_kernel: all tensors must be on a GPU device (got {t.device})")
+    if bias.dtype != torch.int32 or bias.shape != (bias_zmod, H, N, N):
+        raise ValueError(f"qflash_window_kernel: bias must be int32 ({bias_zmod}, {H}, {N}, {N}), got "
+                         f"{tuple(bias.shape)} {bias.dtype}")
+    c = [int(x) for x in consts]
+    _check_i32(sm_rscale=c[0], exp_M=c[1], req_M=c[2], l_M=c[3], acc_M=c[4])
+    L = _lib.load()
+    fl = _lib.Flags(int(flags["EXP_USE_SHIFT"]), int(flags["L_USE_SHIFT"]), int(flags["ACC_USE_SHIFT"]),
+                    int(flags["L_SHIFT"]), int(flags["ACC_SHIFT"]))
+    st = (ctypes.c_int64 * 20)(*q8.stride(), *k8.stride(), *v8.stride(), *o.stride(), *bias.stride())
+    ptr = [ctypes.c_void_p(t.data_ptr()) for t in (q8, k8, v8, o, bias)]
+    rc = L.qflash_hip_window_kernel(*ptr, *c, st, Z, H, N, D, int(bias_zmod), ctypes.byref(fl), _stream_ptr(q8))
+    _lib.check(rc, "qflash_window_kernel")
 
 
 def bench_latency_ms(fn, warmup: float = 10, rep: float = 100, flush_mb: int = 512, device=None) -> float:
@@ -228,6 +263,46 @@ def qflash_forward(
     if return_mode == 'latency':
         return bench_latency_ms(kernel, device=query.device)
     kernel()
+    return o * o_scale
+
+
+def qflash_forward_window(query: Tensor, key: Tensor, value: Tensor, rel_bias: Tensor, mask: Tensor | None = None,
+                          scale: float | None = None) -> Tensor:
+    """QWindowAttention's attention call without the materialised mask.
+
+    Equal, code for code, to ``qflash_forward(query, key, value, attn_mask=M)``
+    with ``M = rel_bias + mask.view(1, nW, 1, N, N).expand(Z // nW, -1, H, -1, -1)
+    .reshape(-1, H, N, N)`` (qflash/attention.py:68-74): every element of M is
+    the fp32 sum rel_bias[0, h, i, j] + mask[z % nW, i, j], so the int32 bias
+    is computed on the (nW, H, N, N) distinct sums only and the kernel reads
+    slice z % nW.  rel_bias: (1, H, N, N); mask: (nW, N, N) or None.
+    """
+    d_q, d_k, d_v = query.shape[-1], key.shape[-1], value.shape[-1]
+    assert d_q == d_k and d_k == d_v
+    assert d_k in {16, 32, 64, 128, 256}
+    if scale is None:
+        scale = 1.0 / (d_q ** 0.5)
+    scale = scale * LOG2E
+    q_scale = query.abs().amax() / INT8_MAX
+    k_scale = key.abs().amax() / INT8_MAX
+    o_scale = value.abs().amax() / INT8_MAX
+    sm_scale = scale * (q_scale * k_scale).item()
+    consts = fixed_point_constants(sm_scale)
+    q8, k8, v8 = quantize(query, q_scale), quantize(key, k_scale), quantize(value, o_scale)
+    o = torch.empty_like(v8)
+    Z, H, N = q8.shape[0], q8.shape[1], q8.shape[2]
+    flag_kw = dict(EXP_USE_SHIFT=EXP_USE_SHIFT, L_USE_SHIFT=L_USE_SHIFT, ACC_USE_SHIFT=ACC_USE_SHIFT,
+                   L_SHIFT=L_SHIFT, ACC_SHIFT=ACC_SHIFT)
+    if mask is None:
+        bias = mask_to_bias(rel_bias, sm_scale, Z, H, N)
+        qflash_masked_kernel[None](q8, k8, v8, o, bias, *consts, *q8.stride(), *k8.stride(), *v8.stride(),
+                                   *o.stride(), *bias.stride(), Z, H, N_CTX=N, HEAD_DIM=d_k, **flag_kw)
+    else:
+        n_win = mask.shape[0]
+        if Z % n_win:
+            raise ValueError(f"batch {Z} is not a multiple of the {n_win} windows of the mask")
+        bias = bias_values(rel_bias + mask.view(n_win, 1, N, N), sm_scale).contiguous()
+        qflash_window_kernel(q8, k8, v8, o, bias, consts, n_win, flag_kw)
     return o * o_scale
 
 

@@ -68,8 +68,10 @@ def relative_position_index(ws: int) -> torch.Tensor:
     return (rel[0] + ws - 1) * (2 * ws - 1) + (rel[1] + ws - 1)
 
 
-def swin_attn_mask(g: torch.Generator, H: int, ws: int, images: int, windows: int) -> torch.Tensor:
-    """(images*windows, H, N, N) fp32 mask = rel-pos bias + shift mask."""
+def swin_parts(g: torch.Generator, H: int, ws: int, windows: int):
+    """QWindowAttention's two mask inputs: the (1, H, N, N) relative-position
+    bias gathered from a (2ws-1)^2 x H table ~ N(0, 0.02), and the (windows, N, N)
+    shift mask (-100 between the 4 regions on the second half of the windows)."""
     N = ws * ws
     table = torch.randn((2 * ws - 1) ** 2, H, generator=g) * 0.02
     bias = table[relative_position_index(ws).view(-1)].view(N, N, H).permute(2, 0, 1).contiguous().unsqueeze(0)
@@ -79,8 +81,25 @@ def swin_attn_mask(g: torch.Generator, H: int, ws: int, images: int, windows: in
     m4 = (region[:, None] != region[None, :]).float() * -100.0
     mask = torch.zeros(windows, N, N)
     mask[windows // 2:] = m4
+    return bias, mask
+
+
+def swin_attn_mask(g: torch.Generator, H: int, ws: int, images: int, windows: int) -> torch.Tensor:
+    """(images*windows, H, N, N) fp32 mask = rel-pos bias + shift mask, composed
+    as QWindowAttention does (qflash/attention.py:68-72)."""
+    N = ws * ws
+    bias, mask = swin_parts(g, H, ws, windows)
     mask = mask.view(1, windows, 1, N, N).expand(images, -1, H, -1, -1)
     return bias + mask.reshape(-1, H, N, N)
+
+
+def make_window_parts(cfg: Config, seed: int):
+    """(rel_bias, shift_mask) of a Swin config, drawn exactly as make_inputs draws
+    the composed mask (same generator sequence after Q, K, V)."""
+    g = torch.Generator().manual_seed(seed)
+    for _ in range(3):
+        outlier_tensor(g, cfg.Z, cfg.H, cfg.N, cfg.D)
+    return swin_parts(g, cfg.H, cfg.window, cfg.windows)
 
 
 def make_inputs(cfg: Config, seed: int, token_major: bool = True):

@@ -155,9 +155,22 @@ def _timm_window_reference(m, x, mask):
     return m.proj((attn @ v).transpose(1, 2).reshape(B_, N, -1))
 
 
+class _WindowRecorder(_Recorder):
+    """Replaces qflash_forward_window: composes the (B_, H, N, N) mask exactly as
+    the reference module does (attention.py:68-72) and records it."""
+
+    def __call__(self, q, k, v, rel_bias, mask=None, scale=None):
+        attn_mask = rel_bias
+        if mask is not None:
+            B_, H, N = q.shape[0], q.shape[1], q.shape[2]
+            nw = mask.shape[0]
+            attn_mask = rel_bias + mask.view(1, nw, 1, N, N).expand(B_ // nw, -1, H, -1, -1).reshape(-1, H, N, N)
+        return super().__call__(q, k, v, attn_mask=attn_mask)
+
+
 def test_window_attention_mask_composition(monkeypatch):
-    rec = _Recorder()
-    monkeypatch.setattr(A.qflash, "forward", rec)
+    rec = _WindowRecorder()
+    monkeypatch.setattr(A, "qflash_forward_window", rec)
     torch.manual_seed(0)
     m = QWindowAttention(48, 3, 7)
     nW, B = 4, 2

@@ -83,6 +83,18 @@ def test_masked_entry_needs_a_bias(lib):
     assert b"attn_bias" in lib.qflash_hip_last_error()
 
 
+def test_window_entry_checks_its_period(lib):
+    st = (ctypes.c_int64 * 20)(*([0] * 20))
+    fake = ctypes.c_void_p(64)
+    rc = lib.qflash_hip_window_kernel(fake, fake, fake, fake, fake, 100, -1, 1, 1, 1, st, 4, 1, 49, 32, 0, None,
+                                      None)
+    assert rc == -1 and b"bias_zmod" in lib.qflash_hip_last_error()
+    rc = lib.qflash_hip_window_kernel(fake, fake, fake, fake, None, 100, -1, 1, 1, 1, st, 4, 1, 49, 32, 2, None, None)
+    assert rc == -1 and b"attn_bias" in lib.qflash_hip_last_error()
+    rc = lib.qflash_hip_window_kernel(fake, fake, fake, fake, fake, 100, -1, 1, 1, 1, st, 4, 1, 49, 16, 2, None, None)
+    assert rc == -2
+
+
 def test_layout_check_rejects_null(lib):
     assert lib.qflash_hip_mfma_layout_check(None, None, None, None) == -1
 

@@ -15,7 +15,7 @@ import torch
 
 from golden_io import load_cases
 from qflash_amd import _lib
-from qflash_amd.kernel import (INT8_MAX, LOG2E, NEG_INF, fixed_point_constants, mask_to_bias, qflash,
+from qflash_amd.kernel import (INT8_MAX, LOG2E, NEG_INF, bias_values, fixed_point_constants, mask_to_bias, qflash,
                                qflash_forward, qflash_kernel, qflash_masked_kernel, quantize)
 
 CASES = load_cases()
@@ -166,3 +166,41 @@ def test_environment_flags_are_read_at_import():
     assert out == ["False", "True", "True", "20", "30"]
     import qflash_amd.kernel as K
     assert (K.EXP_USE_SHIFT, K.L_SHIFT, K.ACC_SHIFT) == (True, 30, 30)
+
+
+def _shift_mask(ws=7):
+    ys, xs = torch.meshgrid(torch.arange(ws), torch.arange(ws), indexing="ij")
+    region = (ys.flatten() >= ws - ws // 2).long() * 2 + (xs.flatten() >= ws - ws // 2).long()
+    return (region[:, None] != region[None, :]).float() * -100.0
+
+
+@pytest.mark.parametrize("sm_scale", [0.0123, 0.09, 0.5])
+def test_window_bias_equals_materialised_bias(sm_scale):
+    """The window path's (nW, H, N, N) bias, indexed by z % nW, equals the bias of
+    the reference's materialised (B_, H, N, N) mask element for element."""
+    g = torch.Generator().manual_seed(4)
+    H, N, nW, B = 3, 49, 4, 3
+    rel = torch.randn(1, H, N, N, generator=g) * 0.02
+    rel[0, 0, :3, :3] = -100.0                       # sums exactly at / beyond the -1e2 boundary
+    rel[0, 1, :3, :3] = 100.0
+    shift = torch.zeros(nW, N, N)
+    shift[nW // 2:] = _shift_mask()
+    shift[1, 5, :] = torch.randn(N, generator=g)     # arbitrary float mask values too
+    full = rel + shift.view(1, nW, 1, N, N).expand(B, -1, H, -1, -1).reshape(-1, H, N, N)
+    want = mask_to_bias(full, sm_scale, B * nW, H, N, materialize=True)
+    compact = bias_values(rel + shift.view(nW, 1, N, N), sm_scale)
+    assert compact.shape == (nW, H, N, N)
+    for z in range(B * nW):
+        assert torch.equal(compact[z % nW], want[z]), z
+
+
+def test_swin_golden_mask_decomposes_into_window_parts():
+    """The golden Swin case's (4, 3, 49, 49) mask is rel_bias + shift mask of 2
+    windows (window 0 unshifted), exactly: the window path sees the same sums."""
+    c = CASES["swin_N49_D32"]
+    full = torch.from_numpy(c["mask"])
+    rel = full[0:1].clone()
+    shift = torch.zeros(2, 49, 49)
+    shift[1] = _shift_mask()
+    composed = rel + shift.view(1, 2, 1, 49, 49).expand(2, -1, 3, -1, -1).reshape(-1, 3, 49, 49)
+    assert torch.equal(composed, full)
