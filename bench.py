@@ -71,7 +71,7 @@ def prepare(cfg_name: str, seed: int, dev, dense_bias: bool = False):
         bias = mask_to_bias(mask.to(dev), sm_scale, cfg.Z, cfg.H, cfg.N, materialize=True)
     o = torch.empty_like(v8)
     return dict(cfg=cfg, q=q, k=k, v=v, mask=mask, q8=q8, k8=k8, v8=v8, o=o, bias=bias, bias_zmod=zmod,
-                consts=consts, o_scale=vs, sm_scale=sm_scale)
+                consts=consts, o_scale=vs, sm_scale=sm_scale, seed=seed)
 
 
 def make_step(w):
@@ -198,9 +198,46 @@ def run_config(name: str, steps: int, warmup: int, dev, seed: int = 0, cpu: bool
            "us_per_call_flushed": flushed_us(step), "tops": cfg.ops / (wall_ms * 1e-3) / 1e12,
            "kernel_tops": cfg.ops / (ev_mean_ms * 1e-3) / 1e12, "sqnr_db": sqnr_db(w, dev),
            "hbm_gbs_algorithmic": cfg.bytes_min / (ev_mean_ms * 1e-3) / 1e9}
+    res["e2e_us"] = e2e_us(w, dev)
     if cpu:
         res["cpu_baseline"] = cpu_baseline(w, host_cores())
     return res
+
+
+def e2e_us(w, dev, reps: int = 10) -> float:
+    """Median wall time of the whole op on fp inputs already on the device:
+    qflash.forward (scales, the host sync, constants, quantisation, bias,
+    kernel, dequantisation), or QWindowAttention's call for Swin configs."""
+    import torch
+
+    from qflash_amd import qflash
+    from qflash_amd.kernel import qflash_forward_window
+    from qflash_amd.workloads import make_window_parts
+
+    cfg = w["cfg"]
+    q, k, v = (x.to(dev, cfg.dtype) for x in (w["q"], w["k"], w["v"]))
+    if w["mask"] is None:
+        def call():
+            return qflash.forward(q, k, v)
+    elif w["bias_zmod"]:
+        rel, shift = (t.to(dev) for t in make_window_parts(cfg, w["seed"]))
+
+        def call():
+            return qflash_forward_window(q, k, v, rel, shift)
+    else:
+        mask = w["mask"].to(dev)
+
+        def call():
+            return qflash.forward(q, k, v, attn_mask=mask)
+    call()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        call()
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t) * 1e6)
+    return statistics.median(times)
 
 
 def main(argv=None):
@@ -272,6 +309,7 @@ def main(argv=None):
                    "timed": "kernel only, int8 Q/K/V resident in HBM"},
         "us_per_call": head["us_per_call"],
         "us_per_call_flushed": head["us_per_call_flushed"],
+        "e2e_us": head["e2e_us"],
         "sqnr_db": head["sqnr_db"],
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_INT8_TOPS, "traffic": traffic,
@@ -288,11 +326,11 @@ def main(argv=None):
         for name in CONFIGS:
             r = head if name == args.config else run_config(name, max(5, args.steps // 5), 3, dev, args.seed)
             per.append({k: r[k] for k in ("config", "us_per_call", "us_per_call_flushed", "kernel_tops",
-                                          "sqnr_db", "hbm_gbs_algorithmic")})
+                                          "sqnr_db", "hbm_gbs_algorithmic", "e2e_us")})
             if CONFIGS[name].swin:  # the reference's materialised (Z, H, N, N) bias, for comparison
                 r = run_config(name, max(5, args.steps // 5), 3, dev, args.seed, dense_bias=True)
                 per.append({k: r[k] for k in ("config", "us_per_call", "us_per_call_flushed", "kernel_tops",
-                                              "sqnr_db", "hbm_gbs_algorithmic")})
+                                              "sqnr_db", "hbm_gbs_algorithmic", "e2e_us")})
         line["per_config"] = per
     print(json.dumps(line), flush=True)
     return 0

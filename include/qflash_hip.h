@@ -83,6 +83,37 @@ int qflash_hip_window_kernel(const int8_t* Q, const int8_t* K, const int8_t* V, 
                              int32_t N_CTX, int32_t HEAD_DIM, int32_t bias_zmod, const qflash_hip_flags* flags,
                              void* stream);
 
+/* Element types of the floating-point inputs of the quantisation entry points. */
+#define QFLASH_HIP_F32 0
+#define QFLASH_HIP_F16 1
+#define QFLASH_HIP_BF16 2
+
+/*
+ * Per-tensor absmax scales of Q, K and V in their own dtype, replacing
+ * `x.abs().amax() / INT8_MAX` and `(q_scale * k_scale)` of qflash_forward
+ * (qflash/kernel.py:294-297) with one read of each input:
+ *   scales[0..2] = amax(|q|), amax(|k|), amax(|v|) times RN_fp32(1/127), rounded
+ *                  to the dtype (torch's division of a device tensor by a host
+ *                  scalar), scales[3] = scales[0] * scales[1] rounded to the dtype.
+ * shapes_strides: for q, k, v in turn, 4 sizes (Z, H, N, D) then 4 element strides.
+ * workspace: device uint32 scratch of at least qflash_hip_scales_workspace()
+ * entries, provided by the caller (the call allocates nothing).
+ */
+int64_t qflash_hip_scales_workspace(const int64_t* shapes_strides);
+int qflash_hip_scales(const void* q, const void* k, const void* v, int32_t dtype, const int64_t* shapes_strides,
+                      void* scales, uint32_t* workspace, int64_t workspace_elems, void* stream);
+
+/*
+ * int8 codes clamp(round(x / scale), -128, 127) of Q, K, V (qflash/kernel.py:
+ * 309-311), scale = scales[0..2] as written by qflash_hip_scales (device
+ * memory, read on the device: no host synchronisation).  The division is IEEE
+ * fp32 (then rounded to the dtype), round half to even.  out_strides: 4 element
+ * strides per output, in the order q8, k8, v8.
+ */
+int qflash_hip_quantize(const void* q, const void* k, const void* v, int32_t dtype, const int64_t* shapes_strides,
+                        int8_t* q8, int8_t* k8, int8_t* v8, const int64_t* out_strides, const void* scales,
+                        void* stream);
+
 /* Message for the last failing call on this thread ("" if none). */
 const char* qflash_hip_last_error(void);
 

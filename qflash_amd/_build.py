@@ -11,8 +11,8 @@ import subprocess
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-SOURCES = [os.path.join(HERE, "csrc", "qflash_fwd.hip")]
-HEADERS = [os.path.join(ROOT, "include", "qflash_hip.h")]
+SOURCES = [os.path.join(HERE, "csrc", "qflash_fwd.hip"), os.path.join(HERE, "csrc", "qflash_quant.hip")]
+HEADERS = [os.path.join(ROOT, "include", "qflash_hip.h"), os.path.join(HERE, "csrc", "qf_error.h")]
 LIB_PATH = os.path.join(HERE, "libqflash_hip.so")
 ARCH = "gfx950"
 

@@ -30,6 +30,7 @@
 #include <string.h>
 
 #include "../../include/qflash_hip.h"
+#include "qf_error.h"
 
 namespace qf {
 
@@ -591,7 +592,7 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
                                           const int8_t* lv, const Frag<D>& fr, const BiasRow& brow, int kstart,
                                           int lane, bool wave_fast, int32_t xlim) {
     constexpr int DB = D / 32;
-    const int lq = lane & 31, g = lane >> 5;
+    const int g = lane >> 5;
     const int32_t rs = a.rs, eM = a.eM, rM = a.rM;
 
     int32_t bias_v[16];
@@ -950,16 +951,8 @@ __global__ __launch_bounds__(64) void mfma_layout_kernel(const int8_t* A, const 
 
 // ----------------------------------------------------------------------------
 // Host side
-static thread_local char g_err[512];
-
-static int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
-static int fail(int code, const char* fmt, ...) {
-    va_list ap;
-    va_start(ap, fmt);
-    vsnprintf(g_err, sizeof(g_err), fmt, ap);
-    va_end(ap);
-    return code;
-}
+using qferr::fail;
+using qferr::g_err;
 
 // ---- occupancy ------------------------------------------------------------
 // The fast kernel runs at its natural occupancy (as many workgroups per CU as

@@ -4,9 +4,10 @@ Mirrors EfficientCompLab/qflash ``qflash/kernel.py`` for this hot path:
 
 * ``qflash_forward`` follows kernel.py:275-351 step for step (asserts, scale,
   per-tensor absmax scales with the one ``.item()`` sync, fixed-point
-  constants in Python double arithmetic, torch quantisation, mask -> int32
-  bias, launch on torch's current stream, ``o * o_scale``), and raises the
-  same exceptions;
+  constants in Python double arithmetic, quantisation, mask -> int32 bias,
+  launch on torch's current stream, ``o * o_scale``), and raises the same
+  exceptions; the scales and the int8 quantisation run as two HIP passes
+  (``quantize_qkv``) with torch's GPU arithmetic;
 * ``qflash_kernel`` / ``qflash_masked_kernel`` are launchers with the
   reference's launch signature (kernel.py:319-326, :339-346) that call the
   gfx950 HIP kernels through the C ABI (include/qflash_hip.h);
@@ -211,6 +212,60 @@ def bench_latency_ms(fn, warmup: float = 10, rep: float = 100, flush_mb: int = 5
     return statistics.median(a.elapsed_time(b) for a, b in zip(s, e))
 
 
+_DT_CODE = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}
+
+
+def quantize_qkv(query: Tensor, key: Tensor, value: Tensor):
+    """Per-tensor scales and int8 codes of Q, K, V on the device (kernel.py:294-311).
+
+    Returns ``(scales, finish)``: ``scales`` is a 4-element device tensor in the
+    inputs' dtype holding q_scale, k_scale, o_scale and q_scale * k_scale
+    (values identical to ``x.abs().amax() / 127`` and their product as torch
+    computes them on the GPU); ``finish()`` launches the quantisation and
+    returns (q8, k8, v8), each laid out like its input (``empty_like``).  The
+    split lets the caller compute the fixed-point constants, which may raise,
+    between the two, in the reference's order.  Two HIP passes replace torch's
+    twelve; dtypes other than fp32 / fp16 / bf16 use the torch sequence.
+    """
+    T = query.dtype
+    for x in (query, key, value):
+        if not x.is_cuda:
+            raise ValueError(f"qflash: all tensors must be on a GPU device (got {x.device})")
+    if T not in _DT_CODE or key.dtype != T or value.dtype != T or query.dim() != 4 or key.dim() != 4 \
+            or value.dim() != 4:
+        q_scale = query.abs().amax() / INT8_MAX
+        k_scale = key.abs().amax() / INT8_MAX
+        o_scale = value.abs().amax() / INT8_MAX
+        scales = torch.stack([q_scale, k_scale, o_scale, q_scale * k_scale])
+
+        def finish_torch():
+            return quantize(query, q_scale), quantize(key, k_scale), quantize(value, o_scale)
+        return scales, finish_torch
+    L = _lib.load()
+    code = _DT_CODE[T]
+    geo = (ctypes.c_int64 * 24)(*query.shape, *query.stride(), *key.shape, *key.stride(), *value.shape,
+                                 *value.stride())
+    n_ws = L.qflash_hip_scales_workspace(geo)
+    if n_ws < 0:
+        raise _lib.QFlashLibraryError(f"qflash_hip_scales_workspace: bad shapes {query.shape}")
+    ws = torch.empty(max(1, n_ws), dtype=torch.int32, device=query.device)
+    scales = torch.empty(4, dtype=T, device=query.device)
+    stream = _stream_ptr(query)
+    ptrs = [ctypes.c_void_p(x.data_ptr()) for x in (query, key, value)]
+    _lib.check(L.qflash_hip_scales(*ptrs, code, geo, ctypes.c_void_p(scales.data_ptr()),
+                                   ctypes.c_void_p(ws.data_ptr()), n_ws, stream), "qflash_hip_scales")
+
+    def finish():
+        q8, k8, v8 = (torch.empty_like(x, dtype=torch.int8) for x in (query, key, value))
+        ost = (ctypes.c_int64 * 12)(*q8.stride(), *k8.stride(), *v8.stride())
+        _lib.check(L.qflash_hip_quantize(*ptrs, code, geo, ctypes.c_void_p(q8.data_ptr()),
+                                         ctypes.c_void_p(k8.data_ptr()), ctypes.c_void_p(v8.data_ptr()), ost,
+                                         ctypes.c_void_p(scales.data_ptr()), _stream_ptr(query)),
+                   "qflash_hip_quantize")
+        return q8, k8, v8
+    return scales, finish
+
+
 def qflash_forward(
     query: Tensor,
     key: Tensor,
@@ -234,13 +289,12 @@ def qflash_forward(
         scale = 1.0 / (d_q ** 0.5)
     scale = scale * LOG2E
 
-    q_scale = query.abs().amax() / INT8_MAX
-    k_scale = key.abs().amax() / INT8_MAX
-    o_scale = value.abs().amax() / INT8_MAX
-    sm_scale = scale * (q_scale * k_scale).item()  # the one host sync, kernel.py:297
+    scales, finish = quantize_qkv(query, key, value)  # kernel.py:294-296 on the device
+    o_scale = scales[2]
+    sm_scale = scale * scales[3].item()  # the one host sync, kernel.py:297
     sm_rscale, exp_M, req_M, l_M, acc_M = fixed_point_constants(sm_scale)
 
-    q8, k8, v8 = quantize(query, q_scale), quantize(key, k_scale), quantize(value, o_scale)
+    q8, k8, v8 = finish()  # kernel.py:309-311
     o = torch.empty_like(v8)
     Z, H, N = q8.shape[0], q8.shape[1], q8.shape[2]
     grid = None  # the HIP library sizes its own launch
@@ -283,12 +337,11 @@ def qflash_forward_window(query: Tensor, key: Tensor, value: Tensor, rel_bias: T
     if scale is None:
         scale = 1.0 / (d_q ** 0.5)
     scale = scale * LOG2E
-    q_scale = query.abs().amax() / INT8_MAX
-    k_scale = key.abs().amax() / INT8_MAX
-    o_scale = value.abs().amax() / INT8_MAX
-    sm_scale = scale * (q_scale * k_scale).item()
+    scales, finish = quantize_qkv(query, key, value)
+    o_scale = scales[2]
+    sm_scale = scale * scales[3].item()
     consts = fixed_point_constants(sm_scale)
-    q8, k8, v8 = quantize(query, q_scale), quantize(key, k_scale), quantize(value, o_scale)
+    q8, k8, v8 = finish()
     o = torch.empty_like(v8)
     Z, H, N = q8.shape[0], q8.shape[1], q8.shape[2]
     flag_kw = dict(EXP_USE_SHIFT=EXP_USE_SHIFT, L_USE_SHIFT=L_USE_SHIFT, ACC_USE_SHIFT=ACC_USE_SHIFT,

@@ -1,0 +1,75 @@
+"""GPU: the device absmax / quantisation passes (qflash_hip_scales, qflash_hip_quantize)
+against torch's own GPU ops, bit for bit (qflash/kernel.py:294-311)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _torch_ref(q, k, v):
+    qs, ks, vs = (x.abs().amax() / 127 for x in (q, k, v))
+    codes = [torch.clamp(torch.round(x / s), -128, 127).to(torch.int8) for x, s in ((q, qs), (k, ks), (v, vs))]
+    return torch.stack([qs, ks, vs, qs * ks]), codes
+
+
+def _layouts(B, H, N, D, dtype, g):
+    """Contiguous (B,H,N,D), token-major views of one qkv buffer (the module
+    path), and a layout with a non-unit head-dim stride."""
+    x = (torch.randn(B, N, 3 * H * D, generator=g) * 3).to(dtype).to(DEV)
+    x[..., :7] *= 8
+    qkv = x.view(B, N, 3, H, D).permute(2, 0, 3, 1, 4)
+    yield "token-major", tuple(qkv.unbind(0))
+    yield "contiguous", tuple(t.contiguous() for t in qkv.unbind(0))
+    t = (torch.randn(B, H, D, N, generator=g)).to(dtype).to(DEV).transpose(-1, -2)
+    yield "column-strided", (t, t * 2, t - 1)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(2, 3, 197, 64), (1, 4, 577, 64), (3, 2, 49, 32), (1, 2, 33, 128)])
+def test_scales_and_codes_match_torch(dtype, shape):
+    from qflash_amd.kernel import quantize_qkv
+    g = torch.Generator().manual_seed(sum(shape))
+    for name, (q, k, v) in _layouts(*shape, dtype, g):
+        want_scales, want_codes = _torch_ref(q, k, v)
+        scales, finish = quantize_qkv(q, k, v)
+        codes = finish()
+        torch.cuda.synchronize()
+        assert scales.dtype == dtype
+        assert torch.equal(scales, want_scales), (name, scales, want_scales)
+        for c, w, x in zip(codes, want_codes, (q, k, v)):
+            assert c.stride() == w.stride() == torch.empty_like(x, dtype=torch.int8).stride(), name
+            assert torch.equal(c, w), name
+
+
+def test_scale_of_a_constant_tensor_and_ties():
+    """Values that land exactly on .5 after the division round half to even."""
+    from qflash_amd.kernel import quantize_qkv
+    q = torch.full((1, 1, 32, 32), 127.0, device=DEV)
+    q[0, 0, 0, :8] = torch.tensor([0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -127.5])
+    k = torch.arange(32 * 32, dtype=torch.float32, device=DEV).view(1, 1, 32, 32) - 500
+    scales, finish = quantize_qkv(q, k, q)
+    want_scales, want_codes = _torch_ref(q, k, q)
+    codes = finish()
+    assert torch.equal(scales, want_scales)
+    for c, w in zip(codes, want_codes):
+        assert torch.equal(c, w)
+
+
+def test_forward_uses_the_device_passes_and_matches_torch_sequence():
+    """qflash.forward (device quantiser) == the attention kernel fed with torch's codes."""
+    from qflash_amd import qflash
+    from qflash_amd.kernel import LOG2E, fixed_point_constants, qflash_kernel
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 197, 3 * 6 * 64, generator=g).to(DEV)
+    q, k, v = x.view(2, 197, 3, 6, 64).permute(2, 0, 3, 1, 4).unbind(0)
+    out = qflash.forward(q, k, v)
+    (qs, ks, vs, qk), (q8, k8, v8) = _torch_ref(q, k, v)
+    consts = fixed_point_constants((1 / 8) * LOG2E * qk.item())
+    o = torch.empty_like(v8)
+    qflash_kernel[None](q8, k8, v8, o, *consts, *q8.stride(), *k8.stride(), *v8.stride(), *o.stride(), 2, 6,
+                        N_CTX=197, HEAD_DIM=64, L_SHIFT=30, ACC_SHIFT=30)
+    torch.cuda.synchronize()
+    assert torch.equal(out, o * vs)
