@@ -35,6 +35,14 @@ extern "C" {
 #define QFLASH_HIP_EHEADDIM (-2)    /* HEAD_DIM unsupported (D=16 fails BLOCK_N<=HEAD_DIM, kernel.py:105) */
 #define QFLASH_HIP_ELAUNCH (-3)     /* the HIP runtime rejected the launch */
 
+/* Element types: floating-point inputs of the quantisation entry points, and
+ * outputs of qflash_hip_forward. */
+#define QFLASH_HIP_F32 0
+#define QFLASH_HIP_F16 1
+#define QFLASH_HIP_BF16 2
+#define QFLASH_HIP_I8 3 /* output: the int8 codes themselves */
+#define QFLASH_HIP_SCALES_WORKSPACE 192
+
 /* Arithmetic-variant switches, kernel.py:30-36 (QFLASH_* environment). */
 typedef struct qflash_hip_flags {
     int32_t exp_use_shift; /* QFLASH_EXP_USE_SHIFT, default 1 */
@@ -83,10 +91,6 @@ int qflash_hip_window_kernel(const int8_t* Q, const int8_t* K, const int8_t* V, 
                              int32_t N_CTX, int32_t HEAD_DIM, int32_t bias_zmod, const qflash_hip_flags* flags,
                              void* stream);
 
-/* Element types of the floating-point inputs of the quantisation entry points. */
-#define QFLASH_HIP_F32 0
-#define QFLASH_HIP_F16 1
-#define QFLASH_HIP_BF16 2
 
 /*
  * Per-tensor absmax scales of Q, K and V in their own dtype, replacing
@@ -96,10 +100,10 @@ int qflash_hip_window_kernel(const int8_t* Q, const int8_t* K, const int8_t* V, 
  *                  to the dtype (torch's division of a device tensor by a host
  *                  scalar), scales[3] = scales[0] * scales[1] rounded to the dtype.
  * shapes_strides: for q, k, v in turn, 4 sizes (Z, H, N, D) then 4 element strides.
- * workspace: device uint32 scratch of at least qflash_hip_scales_workspace()
- * entries, provided by the caller (the call allocates nothing).
+ * workspace: at least QFLASH_HIP_SCALES_WORKSPACE device uint32 entries,
+ * ZERO-INITIALISED by the caller (partial maxima are accumulated there with
+ * atomic max; the call allocates nothing).
  */
-int64_t qflash_hip_scales_workspace(const int64_t* shapes_strides);
 int qflash_hip_scales(const void* q, const void* k, const void* v, int32_t dtype, const int64_t* shapes_strides,
                       void* scales, uint32_t* workspace, int64_t workspace_elems, void* stream);
 
@@ -113,6 +117,22 @@ int qflash_hip_scales(const void* q, const void* k, const void* v, int32_t dtype
 int qflash_hip_quantize(const void* q, const void* k, const void* v, int32_t dtype, const int64_t* shapes_strides,
                         int8_t* q8, int8_t* k8, int8_t* v8, const int64_t* out_strides, const void* scales,
                         void* stream);
+
+/*
+ * One entry point for every case of the forward, used by qflash_forward: the
+ * masks of both masked entries (attn_bias NULL = unmasked; bias_zmod 0 = the
+ * bias has Z slices, > 0 = window-periodic as in qflash_hip_window_kernel),
+ * and the output either as int8 codes (out_dtype QFLASH_HIP_I8, as the
+ * reference kernels write them) or dequantised in place of the reference's
+ * separate `o * o_scale` (qflash/kernel.py:351): Out[...] = RN_T(code *
+ * o_scale) of type out_dtype (F32 / F16 / BF16), o_scale a device scalar of
+ * that type, at the element offsets given by the 4 Out strides.  No
+ * counterpart in the reference: it fuses the dequantisation pass.
+ */
+int qflash_hip_forward(const int8_t* Q, const int8_t* K, const int8_t* V, void* Out, int32_t out_dtype,
+                       const void* o_scale, const int32_t* attn_bias, int32_t bias_zmod, int32_t sm_rscale,
+                       int32_t exp_M, int32_t req_M, int32_t l_M, int32_t acc_M, const int64_t* strides, int32_t Z,
+                       int32_t H, int32_t N_CTX, int32_t HEAD_DIM, const qflash_hip_flags* flags, void* stream);
 
 /* Message for the last failing call on this thread ("" if none). */
 const char* qflash_hip_last_error(void);

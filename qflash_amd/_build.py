@@ -12,7 +12,7 @@ import subprocess
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 SOURCES = [os.path.join(HERE, "csrc", "qflash_fwd.hip"), os.path.join(HERE, "csrc", "qflash_quant.hip")]
-HEADERS = [os.path.join(ROOT, "include", "qflash_hip.h"), os.path.join(HERE, "csrc", "qf_error.h")]
+HEADERS = [os.path.join(ROOT, "include", "qflash_hip.h"), os.path.join(HERE, "csrc", "qf_common.h")]
 LIB_PATH = os.path.join(HERE, "libqflash_hip.so")
 ARCH = "gfx950"
 
@@ -20,7 +20,7 @@ ARCH = "gfx950"
 # are unreliable on the target pool); the host pass warns that it does not
 # know the feature, which is harmless.
 HIPCC_FLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+    f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC", "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
     # MFMA results in VGPRs: the kernels post-process every result with VALU ops

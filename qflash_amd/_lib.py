@@ -30,12 +30,14 @@ class Flags(ctypes.Structure):
                 ("acc_shift", ctypes.c_int32)]
 
 
-EXPORTS = ("qflash_hip_kernel", "qflash_hip_masked_kernel", "qflash_hip_window_kernel", "qflash_hip_scales",
-           "qflash_hip_scales_workspace", "qflash_hip_quantize", "qflash_hip_last_error",
+EXPORTS = ("qflash_hip_kernel", "qflash_hip_masked_kernel", "qflash_hip_window_kernel", "qflash_hip_forward",
+           "qflash_hip_scales",
+           "qflash_hip_quantize", "qflash_hip_last_error",
            "qflash_hip_mfma_layout_check", "qflash_hip_version")
 
-# element type codes of qflash_hip_scales / qflash_hip_quantize
-F32, F16, BF16 = 0, 1, 2
+# element type codes of qflash_hip_scales / qflash_hip_quantize, and its workspace
+F32, F16, BF16, I8 = 0, 1, 2, 3
+SCALES_WORKSPACE = 192
 
 E_HEADDIM = -2
 
@@ -54,12 +56,13 @@ def _declare(L):
     L.qflash_hip_window_kernel.restype = ctypes.c_int
     L.qflash_hip_window_kernel.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i64p, i32, i32, i32, i32, i32,
                                            fp, vp]
-    L.qflash_hip_scales_workspace.restype = ctypes.c_int64
-    L.qflash_hip_scales_workspace.argtypes = [i64p]
     L.qflash_hip_scales.restype = ctypes.c_int
     L.qflash_hip_scales.argtypes = [vp, vp, vp, i32, i64p, vp, vp, ctypes.c_int64, vp]
     L.qflash_hip_quantize.restype = ctypes.c_int
     L.qflash_hip_quantize.argtypes = [vp, vp, vp, i32, i64p, vp, vp, vp, i64p, vp, vp]
+    L.qflash_hip_forward.restype = ctypes.c_int
+    L.qflash_hip_forward.argtypes = [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32, i32, i32, i64p, i32, i32, i32,
+                                     i32, fp, vp]
     L.qflash_hip_last_error.restype = ctypes.c_char_p
     L.qflash_hip_last_error.argtypes = []
     L.qflash_hip_mfma_layout_check.restype = ctypes.c_int

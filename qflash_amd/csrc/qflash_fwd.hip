@@ -22,6 +22,7 @@
 //                      col l%32)
 //   (checked at run time by qflash_hip_mfma_layout_check).
 #include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
 #include <atomic>
 #include <stdint.h>
 #include <stdarg.h>
@@ -30,7 +31,7 @@
 #include <string.h>
 
 #include "../../include/qflash_hip.h"
-#include "qf_error.h"
+#include "qf_common.h"
 
 namespace qf {
 
@@ -64,7 +65,61 @@ struct Args {
     int32_t n_wg;    // workgroups in the grid (XCD-aware order)
     int32_t bias_zmod;  // > 0: the bias of batch index z is bias[z % bias_zmod] (window-periodic)
     int32_t bias_vec;   // bias rows have unit key stride and non-negative strides: 16-byte buffer loads
+    // output: int8 codes at `o` (out_dt == QFLASH_HIP_I8), or RN_T(code * o_scale)
+    // of type out_dt at the same element offsets of `out_t` (qflash/kernel.py:351)
+    void* out_t;
+    int32_t out_dt;
+    const void* o_scale;
 };
+
+__device__ __forceinline__ int out_esize(int dt) { return dt == QFLASH_HIP_I8 ? 1 : (dt == QFLASH_HIP_F32 ? 4 : 2); }
+
+// o * o_scale in torch's arithmetic: the int8 code and the scale as fp32, one
+// rounding to the output type.
+__device__ __forceinline__ float scale_value(const Args& a) {
+    if (a.out_dt == QFLASH_HIP_F32) return *reinterpret_cast<const float*>(a.o_scale);
+    const uint32_t h = *reinterpret_cast<const uint16_t*>(a.o_scale);
+    return a.out_dt == QFLASH_HIP_F16 ? __half2float(__ushort_as_half((unsigned short)h)) : __uint_as_float(h << 16);
+}
+
+// Stores the output element of `code` at element offset voff + soff of the
+// head's output buffer (rsrc covers the head; offsets in elements).
+template <int OUT>
+__device__ __forceinline__ void put_out(__amdgpu_buffer_rsrc_t rsrc, int32_t code, int32_t voff, int32_t soff,
+                                        float os) {
+    if constexpr (OUT == QFLASH_HIP_I8) {
+        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)code, rsrc, voff, soff, 0);
+    } else if constexpr (OUT == QFLASH_HIP_F32) {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint((float)(int8_t)code * os), rsrc, 4 * voff, 4 * soff, 0);
+    } else if constexpr (OUT == QFLASH_HIP_F16) {
+        __builtin_amdgcn_raw_buffer_store_b16(__half_as_ushort(__float2half_rn((float)(int8_t)code * os)), rsrc,
+                                              2 * voff, 2 * soff, 0);
+    } else {
+        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)qf_bf16_bits((float)(int8_t)code * os), rsrc, 2 * voff,
+                                              2 * soff, 0);
+    }
+}
+
+// Calls f.template operator()<OUT>() for the output type of the launch (one
+// uniform branch per wave instead of one per stored element).
+template <typename F>
+__device__ __forceinline__ void with_out_type(int dt, F&& f) {
+    switch (dt) {
+        case QFLASH_HIP_I8: f.template operator()<QFLASH_HIP_I8>(); break;
+        case QFLASH_HIP_F32: f.template operator()<QFLASH_HIP_F32>(); break;
+        case QFLASH_HIP_F16: f.template operator()<QFLASH_HIP_F16>(); break;
+        default: f.template operator()<QFLASH_HIP_BF16>();
+    }
+}
+
+// Buffer over one head's output, ending after row N-1 (element strides so).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t out_rsrc(const Args& a, int z, int h, int D) {
+    const int es = out_esize(a.out_dt);
+    void* base = a.out_dt == QFLASH_HIP_I8 ? (void*)(a.o + z * a.so[0] + h * a.so[1])
+                                           : (void*)((char*)a.out_t + (z * a.so[0] + h * a.so[1]) * es);
+    return __builtin_amdgcn_make_buffer_rsrc(base, 0, ((a.N - 1) * (int32_t)a.so[2] + (D - 1) * (int32_t)a.so[3] + 1) * es,
+                                             0x00020000);
+}
 
 // ----------------------------------------------------------------------------
 // Integer primitives with the reference's (Triton) semantics: int32 wraps,
@@ -207,7 +262,6 @@ __global__ __launch_bounds__(64 * W) void fwd_general(Args a) {
     const int8_t* qb = a.q + z * a.sq[0] + h * a.sq[1];
     const int8_t* kb = a.k + z * a.sk[0] + h * a.sk[1];
     const int8_t* vb = a.v + z * a.sv[0] + h * a.sv[1];
-    int8_t* ob = a.o + z * a.so[0] + h * a.so[1];
 
     // Q^T as the B operand: lane holds query q0+lq, head dims 32*db+16*g+[0,16).
     i32x4 qv[DB];
@@ -280,19 +334,23 @@ __global__ __launch_bounds__(64 * W) void fwd_general(Args a) {
     }
     if (!active) return;
     // kernel.py:176-180: fp32 divide, fp32->int32, int32->int8, rows < N only.
+    const __amdgpu_buffer_rsrc_t orsrc = out_rsrc(a, z, h, D);
+    const float os = a.out_dt == QFLASH_HIP_I8 ? 0.f : scale_value(a);
+    with_out_type(a.out_dt, [&]<int OUT>() {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const int row = crow(v, lane);
-        const int32_t lv = __shfl(l, row);
-        const int orow = q0 + row;
-        if (orow >= a.N) continue;
-        const float lf = (float)lv;
+        for (int v = 0; v < 16; ++v) {
+            const int row = crow(v, lane);
+            const int32_t lv = __shfl(l, row);
+            const int orow = q0 + row;
+            if (orow >= a.N) continue;
+            const float lf = (float)lv;
 #pragma unroll
-        for (int t = 0; t < DB; ++t) {
-            int32_t code = cvt_x86(__fdiv_rn((float)acc[t][v], lf));
-            ob[(int64_t)orow * a.so[2] + (int64_t)(t * 32 + lq) * a.so[3]] = (int8_t)code;
+            for (int t = 0; t < DB; ++t) {
+                int32_t code = cvt_x86(__fdiv_rn((float)acc[t][v], lf));
+                put_out<OUT>(orsrc, code, (int32_t)(orow * a.so[2] + (t * 32 + lq) * a.so[3]), 0, os);
+            }
         }
-    }
+    });
 }
 
 // ----------------------------------------------------------------------------
@@ -752,7 +810,7 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
 // ((N-1)*so2 + D bytes from the head's base, so2 >= D checked by the host)
 // and are dropped by the hardware.
 template <int D>
-__device__ __forceinline__ void fast_store(const FastState<D>& st, const Args& a, int8_t* ob, int lane, int q0) {
+__device__ __forceinline__ void fast_store(const FastState<D>& st, const Args& a, int z, int h, int lane, int q0) {
     constexpr int DB = D / 32;
     const int lq = lane & 31, g = lane >> 5;
     const float b_row = (float)st.l;            // S layout: lane = row
@@ -761,31 +819,33 @@ __device__ __forceinline__ void fast_store(const FastState<D>& st, const Args& a
     const int32_t y_hi = (int32_t)(uint32_t)((uint64_t)__double_as_longlong(y_row) >> 32);
     const bool exact = __any(st.l >= -1 && st.l <= 1);
     const int32_t so2 = (int32_t)a.so[2];
-    const __amdgpu_buffer_rsrc_t rsrc =
-        __builtin_amdgcn_make_buffer_rsrc(ob, 0, (a.N - 1) * so2 + D, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsrc = out_rsrc(a, z, h, D);
+    const float os = a.out_dt == QFLASH_HIP_I8 ? 0.f : scale_value(a);
     const int32_t voff = (q0 + 4 * g) * so2 + lq;
+    with_out_type(a.out_dt, [&]<int OUT>() {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const int row = crow(v, lane);
-        const int32_t soff = (8 * (v >> 2) + (v & 3)) * so2;
-        if (!exact) {
-            const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * row, y_lo);
-            const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * row, y_hi);
-            const double yd = __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+        for (int v = 0; v < 16; ++v) {
+            const int row = crow(v, lane);
+            const int32_t soff = (8 * (v >> 2) + (v & 3)) * so2;
+            if (!exact) {
+                const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * row, y_lo);
+                const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * row, y_hi);
+                const double yd = __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 #pragma unroll
-            for (int t = 0; t < DB; ++t) {
-                const float qf = (float)((double)(float)st.acc[t][v] * yd);
-                __builtin_amdgcn_raw_buffer_store_b8((uint8_t)(int32_t)qf, rsrc, voff + t * 32, soff, 0);
-            }
-        } else {
-            const float bf = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * row, __float_as_int(b_row)));
+                for (int t = 0; t < DB; ++t) {
+                    const float qf = (float)((double)(float)st.acc[t][v] * yd);
+                    put_out<OUT>(rsrc, (int32_t)qf, voff + t * 32, soff, os);
+                }
+            } else {
+                const float bf = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * row, __float_as_int(b_row)));
 #pragma unroll
-            for (int t = 0; t < DB; ++t) {
-                const int32_t code = cvt_x86(__fdiv_rn((float)st.acc[t][v], bf));
-                __builtin_amdgcn_raw_buffer_store_b8((uint8_t)code, rsrc, voff + t * 32, soff, 0);
+                for (int t = 0; t < DB; ++t) {
+                    const int32_t code = cvt_x86(__fdiv_rn((float)st.acc[t][v], bf));
+                    put_out<OUT>(rsrc, code, voff + t * 32, soff, os);
+                }
             }
         }
-    }
+    });
 }
 
 // The 32 query rows of one wave: K / V stages double-buffered in LDS (the
@@ -796,7 +856,7 @@ __device__ __forceinline__ void fast_store(const FastState<D>& st, const Args& a
 // barriers, active or not.
 template <int D, int W, bool MASKED, bool WIDE, bool DYN>
 __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t* smem, const int8_t* kb,
-                                          const int8_t* vb, int8_t* ob, const BiasRow& brow, int wave, int lane,
+                                          const int8_t* vb, int z, int h, const BiasRow& brow, int wave, int lane,
                                           int q0, bool active, bool wave_fast, int32_t xlim) {
     using S = Stage<D>;
     constexpr int DB = D / 32;
@@ -852,7 +912,7 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
                                                          xlim);
     }
     if (!active) return;
-    fast_store<D>(st, a, ob, lane, q0);
+    fast_store<D>(st, a, z, h, lane, q0);
 }
 
 // Occupancy target (waves per SIMD) by head dim: the register budget of the
@@ -879,7 +939,6 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
     const int8_t* qb = a.q + z * a.sq[0] + h * a.sq[1];
     const int8_t* kb = a.k + z * a.sk[0] + h * a.sk[1];
     const int8_t* vb = a.v + z * a.sv[0] + h * a.sv[1];
-    int8_t* ob = a.o + z * a.so[0] + h * a.so[1];
     BiasRow brow;
     if constexpr (MASKED) {
         const int32_t* bh = a.bias + (a.bias_zmod ? z % a.bias_zmod : z) * a.sb[0] + h * a.sb[1];
@@ -931,11 +990,11 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
     // writes its own rows, so the two never merge register state.
     if constexpr (!MASKED) {
         if (wave_fast)
-            fast_rows<D, W, false, false, DYN>(a, qv, smem, kb, vb, ob, brow, wave, lane, q0, active, wave_fast, xlim);
+            fast_rows<D, W, false, false, DYN>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active, wave_fast, xlim);
         else
-            fast_rows<D, W, false, true, DYN>(a, qv, smem, kb, vb, ob, brow, wave, lane, q0, active, wave_fast, xlim);
+            fast_rows<D, W, false, true, DYN>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active, wave_fast, xlim);
     } else {
-        fast_rows<D, W, true, true, DYN>(a, qv, smem, kb, vb, ob, brow, wave, lane, q0, active, wave_fast, xlim);
+        fast_rows<D, W, true, true, DYN>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active, wave_fast, xlim);
     }
 }
 
@@ -1082,12 +1141,15 @@ static bool getenv_flag(const char* name) {
     return v && v[0] && v[0] != '0';
 }
 
-static int forward(const int8_t* Q, const int8_t* K, const int8_t* V, int8_t* O, const int32_t* bias,
+static int forward(const int8_t* Q, const int8_t* K, const int8_t* V, void* O, const int32_t* bias,
                    int32_t rs, int32_t eM, int32_t rM, int32_t lM, int32_t aM, const int64_t* strides,
                    int32_t Z, int32_t H, int32_t N, int32_t D, const qflash_hip_flags* flags, void* stream,
-                   int32_t bias_zmod = 0) {
+                   int32_t bias_zmod = 0, int32_t out_dt = QFLASH_HIP_I8, const void* o_scale = nullptr) {
     g_err[0] = 0;
     if (!Q || !K || !V || !O || !strides) return fail(QFLASH_HIP_EINVAL, "null pointer argument");
+    if (out_dt != QFLASH_HIP_I8 && out_dt != QFLASH_HIP_F32 && out_dt != QFLASH_HIP_F16 && out_dt != QFLASH_HIP_BF16)
+        return fail(QFLASH_HIP_EINVAL, "unknown output dtype code %d", out_dt);
+    if (out_dt != QFLASH_HIP_I8 && !o_scale) return fail(QFLASH_HIP_EINVAL, "o_scale is null");
     if (Z <= 0 || H <= 0 || N <= 0) return fail(QFLASH_HIP_EINVAL, "bad shape Z=%d H=%d N=%d", Z, H, N);
     if (D == 16)
         return fail(QFLASH_HIP_EHEADDIM, "HEAD_DIM=16 < BLOCK_N=32: the reference kernel rejects it "
@@ -1102,9 +1164,20 @@ static int forward(const int8_t* Q, const int8_t* K, const int8_t* V, int8_t* O,
     if (f.acc_use_shift && (f.acc_shift < 1 || f.acc_shift > 62))
         return fail(QFLASH_HIP_EINVAL, "acc_shift %d outside 1..62", f.acc_shift);
     if ((int64_t)Z * H > (int64_t)INT32_MAX / 64) return fail(QFLASH_HIP_EINVAL, "Z*H too large");
+    // the output of one head is written through a buffer resource: byte offsets in 32 bits
+    for (int i = 0; i < 4; ++i)
+        if (strides[12 + i] < 0) return fail(QFLASH_HIP_EINVAL, "negative output stride");
+    if (((int64_t)(N - 1) * strides[14] + (int64_t)(D - 1) * strides[15] + 1) *
+            (out_dt == QFLASH_HIP_I8 ? 1 : (out_dt == QFLASH_HIP_F32 ? 4 : 2)) >
+        INT32_MAX)
+        return fail(QFLASH_HIP_EINVAL, "one head's output spans more than 2 GiB");
 
     Args a;
-    a.q = Q; a.k = K; a.v = V; a.o = O; a.bias = bias;
+    a.q = Q; a.k = K; a.v = V; a.bias = bias;
+    a.o = out_dt == QFLASH_HIP_I8 ? (int8_t*)O : nullptr;
+    a.out_t = out_dt == QFLASH_HIP_I8 ? nullptr : O;
+    a.out_dt = out_dt;
+    a.o_scale = o_scale;
     for (int i = 0; i < 4; ++i) {
         a.sq[i] = strides[i];
         a.sk[i] = strides[4 + i];
@@ -1194,6 +1267,16 @@ int qflash_hip_window_kernel(const int8_t* Q, const int8_t* K, const int8_t* V, 
     if (bias_zmod < 1) return qf::fail(QFLASH_HIP_EINVAL, "bias_zmod must be >= 1 (got %d)", bias_zmod);
     return qf::forward(Q, K, V, Out, attn_bias, sm_rscale, exp_M, req_M, l_M, acc_M, strides, Z, H, N_CTX,
                        HEAD_DIM, flags, stream, bias_zmod);
+}
+
+int qflash_hip_forward(const int8_t* Q, const int8_t* K, const int8_t* V, void* Out, int32_t out_dtype,
+                       const void* o_scale, const int32_t* attn_bias, int32_t bias_zmod, int32_t sm_rscale,
+                       int32_t exp_M, int32_t req_M, int32_t l_M, int32_t acc_M, const int64_t* strides, int32_t Z,
+                       int32_t H, int32_t N_CTX, int32_t HEAD_DIM, const qflash_hip_flags* flags, void* stream) {
+    if (bias_zmod < 0 || (bias_zmod > 0 && !attn_bias))
+        return qf::fail(QFLASH_HIP_EINVAL, "bias_zmod %d needs a bias (>= 0)", bias_zmod);
+    return qf::forward(Q, K, V, Out, attn_bias, sm_rscale, exp_M, req_M, l_M, acc_M, strides, Z, H, N_CTX, HEAD_DIM,
+                       flags, stream, bias_zmod, out_dtype, o_scale);
 }
 
 const char* qflash_hip_last_error(void) { return qf::g_err; }

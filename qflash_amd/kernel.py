@@ -245,15 +245,12 @@ def quantize_qkv(query: Tensor, key: Tensor, value: Tensor):
     code = _DT_CODE[T]
     geo = (ctypes.c_int64 * 24)(*query.shape, *query.stride(), *key.shape, *key.stride(), *value.shape,
                                  *value.stride())
-    n_ws = L.qflash_hip_scales_workspace(geo)
-    if n_ws < 0:
-        raise _lib.QFlashLibraryError(f"qflash_hip_scales_workspace: bad shapes {query.shape}")
-    ws = torch.empty(max(1, n_ws), dtype=torch.int32, device=query.device)
+    ws = torch.zeros(_lib.SCALES_WORKSPACE, dtype=torch.int32, device=query.device)  # atomic max from 0
     scales = torch.empty(4, dtype=T, device=query.device)
     stream = _stream_ptr(query)
     ptrs = [ctypes.c_void_p(x.data_ptr()) for x in (query, key, value)]
     _lib.check(L.qflash_hip_scales(*ptrs, code, geo, ctypes.c_void_p(scales.data_ptr()),
-                                   ctypes.c_void_p(ws.data_ptr()), n_ws, stream), "qflash_hip_scales")
+                                   ctypes.c_void_p(ws.data_ptr()), ws.numel(), stream), "qflash_hip_scales")
 
     def finish():
         q8, k8, v8 = (torch.empty_like(x, dtype=torch.int8) for x in (query, key, value))
@@ -264,6 +261,42 @@ def quantize_qkv(query: Tensor, key: Tensor, value: Tensor):
                    "qflash_hip_quantize")
         return q8, k8, v8
     return scales, finish
+
+
+def launch_forward(q8: Tensor, k8: Tensor, v8: Tensor, out: Tensor, consts, flags: dict, bias: Tensor | None = None,
+                   bias_zmod: int = 0, o_scale: Tensor | None = None) -> None:
+    """One launch of the integer forward through qflash_hip_forward.
+
+    ``out`` is int8 (the codes) or fp32 / fp16 / bf16: then it receives
+    ``code * o_scale`` rounded to its dtype, the reference's final ``o * o_scale``
+    (kernel.py:351) fused into the kernel; ``o_scale`` is a device scalar of
+    that dtype.  ``bias``: None, (Z, H, N, N) strided, or (bias_zmod, H, N, N)
+    window-periodic.
+    """
+    Z, H, N, D = q8.shape
+    for t in (q8, k8, v8, out) + (() if bias is None else (bias,)):
+        if not t.is_cuda:
+            raise ValueError(f"qflash: all tensors must be on a GPU device (got {t.device})")
+    if out.dtype == torch.int8:
+        code, sp = _lib.I8, None
+    else:
+        code = _DT_CODE.get(out.dtype)
+        if code is None or o_scale is None or o_scale.dtype != out.dtype or not o_scale.is_cuda:
+            raise ValueError("qflash: a dequantised output needs a device o_scale of the output dtype "
+                             f"(fp32 / fp16 / bf16), got {out.dtype} and {o_scale}")
+        sp = ctypes.c_void_p(o_scale.data_ptr())
+    c = [int(x) for x in consts]
+    _check_i32(sm_rscale=c[0], exp_M=c[1], req_M=c[2], l_M=c[3], acc_M=c[4])
+    L = _lib.load()
+    fl = _lib.Flags(int(flags["EXP_USE_SHIFT"]), int(flags["L_USE_SHIFT"]), int(flags["ACC_USE_SHIFT"]),
+                    int(flags["L_SHIFT"]), int(flags["ACC_SHIFT"]))
+    bst = (0, 0, 0, 0) if bias is None else bias.stride()
+    st = (ctypes.c_int64 * 20)(*q8.stride(), *k8.stride(), *v8.stride(), *out.stride(), *bst)
+    bp = None if bias is None else ctypes.c_void_p(bias.data_ptr())
+    rc = L.qflash_hip_forward(ctypes.c_void_p(q8.data_ptr()), ctypes.c_void_p(k8.data_ptr()),
+                              ctypes.c_void_p(v8.data_ptr()), ctypes.c_void_p(out.data_ptr()), code, sp, bp,
+                              int(bias_zmod), *c, st, Z, H, N, D, ctypes.byref(fl), _stream_ptr(q8))
+    _lib.check(rc, "qflash_hip_forward")
 
 
 def qflash_forward(
@@ -295,28 +328,21 @@ def qflash_forward(
     sm_rscale, exp_M, req_M, l_M, acc_M = fixed_point_constants(sm_scale)
 
     q8, k8, v8 = finish()  # kernel.py:309-311
-    o = torch.empty_like(v8)
     Z, H, N = q8.shape[0], q8.shape[1], q8.shape[2]
-    grid = None  # the HIP library sizes its own launch
+    consts = (sm_rscale, exp_M, req_M, l_M, acc_M)
     flag_kw = dict(EXP_USE_SHIFT=EXP_USE_SHIFT, L_USE_SHIFT=L_USE_SHIFT, ACC_USE_SHIFT=ACC_USE_SHIFT,
                    L_SHIFT=L_SHIFT, ACC_SHIFT=ACC_SHIFT)
+    bias = None if attn_mask is None else mask_to_bias(attn_mask, sm_scale, Z, H, N)
 
-    if attn_mask is None:
-        def kernel():
-            qflash_kernel[grid](q8, k8, v8, o, sm_rscale, exp_M, req_M, l_M, acc_M,
-                                *q8.stride(), *k8.stride(), *v8.stride(), *o.stride(),
-                                Z, H, N_CTX=N, HEAD_DIM=d_k, **flag_kw)
-    else:
-        bias = mask_to_bias(attn_mask, sm_scale, Z, H, N)
-
-        def kernel():
-            qflash_masked_kernel[grid](q8, k8, v8, o, bias, sm_rscale, exp_M, req_M, l_M, acc_M,
-                                       *q8.stride(), *k8.stride(), *v8.stride(), *o.stride(), *bias.stride(),
-                                       Z, H, N_CTX=N, HEAD_DIM=d_k, **flag_kw)
-
-    if return_mode == 'latency':
-        return bench_latency_ms(kernel, device=query.device)
-    kernel()
+    if return_mode == 'latency':  # the kernel alone, int8 codes out (kernel.py:348-349)
+        o = torch.empty_like(v8)
+        return bench_latency_ms(lambda: launch_forward(q8, k8, v8, o, consts, flag_kw, bias), device=query.device)
+    if o_scale.dtype in _DT_CODE:  # o * o_scale fused into the kernel's stores
+        out = torch.empty_like(v8, dtype=o_scale.dtype)
+        launch_forward(q8, k8, v8, out, consts, flag_kw, bias, o_scale=o_scale)
+        return out
+    o = torch.empty_like(v8)
+    launch_forward(q8, k8, v8, o, consts, flag_kw, bias)
     return o * o_scale
 
 
@@ -347,15 +373,17 @@ def qflash_forward_window(query: Tensor, key: Tensor, value: Tensor, rel_bias: T
     flag_kw = dict(EXP_USE_SHIFT=EXP_USE_SHIFT, L_USE_SHIFT=L_USE_SHIFT, ACC_USE_SHIFT=ACC_USE_SHIFT,
                    L_SHIFT=L_SHIFT, ACC_SHIFT=ACC_SHIFT)
     if mask is None:
-        bias = mask_to_bias(rel_bias, sm_scale, Z, H, N)
-        qflash_masked_kernel[None](q8, k8, v8, o, bias, *consts, *q8.stride(), *k8.stride(), *v8.stride(),
-                                   *o.stride(), *bias.stride(), Z, H, N_CTX=N, HEAD_DIM=d_k, **flag_kw)
+        bias, zmod = mask_to_bias(rel_bias, sm_scale, Z, H, N), 0
     else:
         n_win = mask.shape[0]
         if Z % n_win:
             raise ValueError(f"batch {Z} is not a multiple of the {n_win} windows of the mask")
-        bias = bias_values(rel_bias + mask.view(n_win, 1, N, N), sm_scale).contiguous()
-        qflash_window_kernel(q8, k8, v8, o, bias, consts, n_win, flag_kw)
+        bias, zmod = bias_values(rel_bias + mask.view(n_win, 1, N, N), sm_scale).contiguous(), n_win
+    if o_scale.dtype in _DT_CODE:  # o * o_scale fused into the kernel's stores
+        out = torch.empty_like(v8, dtype=o_scale.dtype)
+        launch_forward(q8, k8, v8, out, consts, flag_kw, bias, zmod, o_scale=o_scale)
+        return out
+    launch_forward(q8, k8, v8, o, consts, flag_kw, bias, zmod)
     return o * o_scale
 
 

@@ -118,3 +118,34 @@ def test_header_compiles_as_c_and_cxx(tmp_path):
         exe = tmp_path / ("a_" + cc[0])
         subprocess.run([*cc, "-Wall", "-Werror", "-I", inc, str(src), "-o", str(exe)], check=True)
         subprocess.run([str(exe)], check=True)
+
+
+def test_forward_entry_checks_output_and_bias(lib):
+    st = (ctypes.c_int64 * 20)(*([0] * 20))
+    fake = ctypes.c_void_p(64)
+    args = [100, -1, 1, 1, 1, st, 1, 1, 32, 64, None, None]
+    # unknown output dtype; dequantised output without o_scale; bias period without a bias
+    assert lib.qflash_hip_forward(fake, fake, fake, fake, 7, fake, None, 0, *args) == -1
+    assert b"output dtype" in lib.qflash_hip_last_error()
+    assert lib.qflash_hip_forward(fake, fake, fake, fake, _lib.F16, None, None, 0, *args) == -1
+    assert b"o_scale" in lib.qflash_hip_last_error()
+    assert lib.qflash_hip_forward(fake, fake, fake, fake, _lib.I8, None, None, 4, *args) == -1
+    assert b"bias_zmod" in lib.qflash_hip_last_error()
+    args[8] = 16
+    assert lib.qflash_hip_forward(fake, fake, fake, fake, _lib.I8, None, None, 0, *args) == -2
+
+
+def test_quantiser_entries_check_arguments(lib):
+    geo = (ctypes.c_int64 * 24)(*([1, 1, 4, 32, 128, 128, 32, 1] * 3))
+    fake = ctypes.c_void_p(64)
+    ws = ctypes.c_void_p(64)
+    assert lib.qflash_hip_scales(fake, fake, fake, 9, geo, fake, ws, 192, None) == -1
+    assert b"dtype" in lib.qflash_hip_last_error()
+    assert lib.qflash_hip_scales(fake, fake, fake, _lib.F32, geo, fake, ws, 3, None) == -1
+    assert b"workspace" in lib.qflash_hip_last_error()
+    bad = (ctypes.c_int64 * 24)(*([1, 1, 0, 32, 128, 128, 32, 1] * 3))
+    assert lib.qflash_hip_scales(fake, fake, fake, _lib.F32, bad, fake, ws, 192, None) == -1
+    assert b"empty" in lib.qflash_hip_last_error()
+    ost = (ctypes.c_int64 * 12)(*([128, 128, 32, 1] * 3))
+    assert lib.qflash_hip_quantize(fake, fake, fake, _lib.F32, geo, None, fake, fake, ost, fake, None) == -1
+    assert b"null" in lib.qflash_hip_last_error()

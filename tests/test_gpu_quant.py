@@ -73,3 +73,37 @@ def test_forward_uses_the_device_passes_and_matches_torch_sequence():
                         N_CTX=197, HEAD_DIM=64, L_SHIFT=30, ACC_SHIFT=30)
     torch.cuda.synchronize()
     assert torch.equal(out, o * vs)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("masked", [False, True])
+def test_fused_dequantisation_equals_codes_times_scale(dtype, masked):
+    """The kernel's fused `o * o_scale` (fp32 / fp16 / bf16 stores) equals torch's
+    product of the int8 codes with the scale, for the fast and general kernels."""
+    from qflash_amd.kernel import (LOG2E, fixed_point_constants, launch_forward, mask_to_bias, quantize_qkv)
+    g = torch.Generator().manual_seed(8)
+    Z, H, N, D = 2, 3, 100, 64
+    q, k, v = ((torch.randn(Z, N, H, D, generator=g) * 2).to(dtype).to(DEV).permute(0, 2, 1, 3) for _ in range(3))
+    scales, finish = quantize_qkv(q, k, v)
+    consts = fixed_point_constants((1 / 8) * LOG2E * scales[3].item())
+    q8, k8, v8 = finish()
+    bias = None
+    if masked:
+        m = torch.rand(N, N, generator=g) > 0.2
+        bias = mask_to_bias(m.to(DEV), 0.01, Z, H, N)
+    flags = dict(EXP_USE_SHIFT=True, L_USE_SHIFT=True, ACC_USE_SHIFT=True, L_SHIFT=30, ACC_SHIFT=30)
+    for general in (False, True):
+        import os
+        if general:
+            os.environ["QFLASH_HIP_FORCE_GENERAL"] = "1"
+        try:
+            o8 = torch.empty_like(v8)
+            launch_forward(q8, k8, v8, o8, consts, flags, bias)
+            out = torch.empty_like(v8, dtype=dtype)
+            launch_forward(q8, k8, v8, out, consts, flags, bias, o_scale=scales[2])
+        finally:
+            os.environ.pop("QFLASH_HIP_FORCE_GENERAL", None)
+        torch.cuda.synchronize()
+        want = o8 * scales[2]
+        assert want.dtype == dtype and want.stride() == out.stride()
+        assert torch.equal(out, want), (dtype, masked, general)
