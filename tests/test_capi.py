@@ -131,7 +131,7 @@ def test_forward_entry_checks_output_and_bias(lib):
     assert b"o_scale" in lib.qflash_hip_last_error()
     assert lib.qflash_hip_forward(fake, fake, fake, fake, _lib.I8, None, None, 4, *args) == -1
     assert b"bias_zmod" in lib.qflash_hip_last_error()
-    args[8] = 16
+    args[9] = 16
     assert lib.qflash_hip_forward(fake, fake, fake, fake, _lib.I8, None, None, 0, *args) == -2
 
 
