@@ -146,6 +146,18 @@ const char* qflash_hip_last_error(void);
 int qflash_hip_mfma_layout_check(const int8_t* A, const int8_t* B, int32_t* C, void* stream);
 
 /* Library version string (no counterpart in the reference). */
+/*
+ * Diagnostic, no counterpart in the reference: the bounds of the table that
+ * the fast kernel may use for exp2 + requantisation under these constants
+ * (shift variant of exp2).  lut_n: entries p(0 .. lut_n-1) with
+ * p(u) = int8(requant(exp2(-u))) as in qflash/kernel.py:40-64, the last one 0
+ * (0 = no table: the kernel computes p arithmetically); lut_lim: p(u) == 0 for
+ * every u in [lut_n-1, lut_lim].  The kernel caps lut_lim at its table size
+ * and uses the table for launches large enough to repay filling it.
+ * Host-only, needs no GPU.
+ */
+int qflash_hip_lut_bounds(int32_t sm_rscale, int32_t exp_M, int32_t req_M, int32_t* lut_n, int32_t* lut_lim);
+
 const char* qflash_hip_version(void);
 
 #ifdef __cplusplus

@@ -33,7 +33,7 @@ class Flags(ctypes.Structure):
 EXPORTS = ("qflash_hip_kernel", "qflash_hip_masked_kernel", "qflash_hip_window_kernel", "qflash_hip_forward",
            "qflash_hip_scales",
            "qflash_hip_quantize", "qflash_hip_last_error",
-           "qflash_hip_mfma_layout_check", "qflash_hip_version")
+           "qflash_hip_mfma_layout_check", "qflash_hip_lut_bounds", "qflash_hip_version")
 
 # element type codes of qflash_hip_scales / qflash_hip_quantize, and its workspace
 F32, F16, BF16, I8 = 0, 1, 2, 3
@@ -67,6 +67,8 @@ def _declare(L):
     L.qflash_hip_last_error.argtypes = []
     L.qflash_hip_mfma_layout_check.restype = ctypes.c_int
     L.qflash_hip_mfma_layout_check.argtypes = [vp, vp, vp, vp]
+    L.qflash_hip_lut_bounds.restype = ctypes.c_int
+    L.qflash_hip_lut_bounds.argtypes = [i32, i32, i32, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]
     L.qflash_hip_version.restype = ctypes.c_char_p
     L.qflash_hip_version.argtypes = []
 

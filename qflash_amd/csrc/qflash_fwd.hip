@@ -43,6 +43,7 @@ constexpr int32_t kNegInf = -(1 << 20);  // kernel.py:137
 #define QF_FAST_WAVES_D64 4
 #endif
 constexpr int kBN = 32;                   // kernel.py:27, one rescale step
+constexpr int kLutMax = 8192;             // bytes of LDS for the p(u) table of the fast kernel
 
 struct Args {
     const int8_t* q;
@@ -65,6 +66,10 @@ struct Args {
     int32_t n_wg;    // workgroups in the grid (XCD-aware order)
     int32_t bias_zmod;  // > 0: the bias of batch index z is bias[z % bias_zmod] (window-periodic)
     int32_t bias_vec;   // bias rows have unit key stride and non-negative strides: 16-byte buffer loads
+    // exp2 + requantisation by table (see lut_pack_vt): p(u) = lut[min(u, lut_n - 1)]
+    // for u = m' - s in [0, lut_lim]
+    int32_t lut_n;      // table entries (the last one 0), 0 = no table
+    int32_t lut_lim;
     // output: int8 codes at `o` (out_dt == QFLASH_HIP_I8), or RN_T(code * o_scale)
     // of type out_dt at the same element offsets of `out_t` (qflash/kernel.py:351)
     void* out_t;
@@ -126,22 +131,22 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t out_rsrc(const Args& a, int z,
 // `>>` by a count >= 32 (read as unsigned) gives the sign fill, `//`
 // truncates.  AMD's 32-bit shifts use only the low 5 bits of the count, so
 // the clamp is explicit.
-__device__ __forceinline__ int32_t wadd(int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); }
-__device__ __forceinline__ int32_t wsub(int32_t a, int32_t b) { return (int32_t)((uint32_t)a - (uint32_t)b); }
-__device__ __forceinline__ int32_t wmul(int32_t a, int32_t b) { return (int32_t)((uint32_t)a * (uint32_t)b); }
-__device__ __forceinline__ int32_t sra(int32_t a, int32_t b) {
+__host__ __device__ __forceinline__ int32_t wadd(int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); }
+__host__ __device__ __forceinline__ int32_t wsub(int32_t a, int32_t b) { return (int32_t)((uint32_t)a - (uint32_t)b); }
+__host__ __device__ __forceinline__ int32_t wmul(int32_t a, int32_t b) { return (int32_t)((uint32_t)a * (uint32_t)b); }
+__host__ __device__ __forceinline__ int32_t sra(int32_t a, int32_t b) {
     return (uint32_t)b > 31u ? (a >> 31) : (a >> b);
 }
 
 // exp2_i32: kernel.py:40-59.
-__device__ __forceinline__ int32_t exp2_i32(int32_t x, const Args& a) {
+__host__ __device__ __forceinline__ int32_t exp2_i32(int32_t x, const Args& a) {
     int32_t q = a.exp_mode ? (wmul(x, a.eM) >> 16) : (wsub(0, x) / a.rs);
     int32_t r = wadd(x, wmul(q, a.rs));
     return sra(wadd(r >> 1, a.rs), q);
 }
 
 // requantize: kernel.py:62-64 (int8 wrap of the rounded product).
-__device__ __forceinline__ int32_t requant(int32_t e, const Args& a) {
+__host__ __device__ __forceinline__ int32_t requant(int32_t e, const Args& a) {
     return (int32_t)(int8_t)(wadd(wmul(e, a.rM), 1 << 15) >> 16);
 }
 
@@ -377,6 +382,7 @@ __global__ __launch_bounds__(64 * W) void fwd_general(Args a) {
 // 64-bit multiply-add per element.
 __device__ __forceinline__ int32_t mad24(int32_t a, int32_t b, int32_t c) { return __mul24(a, b) + c; }
 __device__ __forceinline__ int32_t max3(int32_t a, int32_t b, int32_t c) { return max(max(a, b), c); }
+__device__ __forceinline__ int32_t min3(int32_t a, int32_t b, int32_t c) { return min(min(a, b), c); }
 
 // K / V stages of 64 keys (two rescale steps) per LDS buffer.  Both tiles
 // hold rows of D bytes exactly as in HBM, copied there by buffer loads that
@@ -565,6 +571,169 @@ __device__ __forceinline__ int32_t exp2_fast(int32_t x, int32_t eM, int32_t rs) 
     return av >> min((uint32_t)q1, 31u);
 }
 
+// exp2 + requantisation by table lookup.  For x = s - m' = -u the
+// reference's p(x) = int8(requant(exp2(x))) depends on u alone, and past a
+// host-computed point it is 0 over a long range: with q = floor(u*|eM| / 2^16)
+// (no int32 wrap while u*|eM| < 2^31) and kappa = |eM|*rs - 2^16, the
+// remainder r = q*rs - u lies in (u*kappa/2^16 - rs, u*kappa/2^16], so
+// E = ((r >> 1) + rs) >> q is 0 once 2^q exceeds rs + max(0, r/2) (true for
+// q >= bitlen(rs) + 3 when kappa <= 2|eM|) as long as r >= -2rs (all u when
+// kappa >= 0, u <= rs*2^16/|kappa| otherwise); p(E = 0) = 0.  The table holds
+// p(u) for u = 0 .. lut_n - 1 (its last entry 0), every u up to lut_lim reads
+// entry min(u, lut_n - 1), and a step uses the table only when all of its
+// real columns have u <= lut_lim.  Clamping also makes the many far-off
+// columns of a step read one byte (a broadcast, no LDS bank conflict): with
+// the addresses left spread over a table of 8 KB the kernel is slower
+// (measured).  The table lives in LDS after the K / V
+// stages; `addr` are LDS byte addresses.  Each byte load fills bits 0-7 of
+// its own register (the half-register d16 loads are no use here: with
+// SRAM ECC on, as on MI355X, they clear the other half), and three
+// shift-ors pack four p values into the MFMA A operand's byte order.  The
+// step's V^T fragment reads (read_vt) go out in the same asm block, so one
+// LDS wait covers both; the compiler's own packing of byte loads would take
+// 4.5 instructions per four bytes, and it would wait for the in-flight
+// stage copy before every LDS read.
+template <int D>
+__device__ __forceinline__ void lut_pack_vt(uint32_t* pk, i32x4* vf, const uint32_t* addr, const int8_t* lv,
+                                            const Frag<D>& fr) {
+    typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+    const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)lv;
+    uint32_t r[16];
+    i32x2 t[2 * (D / 32)];
+    if constexpr (D == 32) {
+        asm volatile(
+            "ds_read_u8 %0, %18\n\t"
+            "ds_read_u8 %1, %19\n\t"
+            "ds_read_u8 %2, %20\n\t"
+            "ds_read_u8 %3, %21\n\t"
+            "ds_read_u8 %4, %22\n\t"
+            "ds_read_u8 %5, %23\n\t"
+            "ds_read_u8 %6, %24\n\t"
+            "ds_read_u8 %7, %25\n\t"
+            "ds_read_u8 %8, %26\n\t"
+            "ds_read_u8 %9, %27\n\t"
+            "ds_read_u8 %10, %28\n\t"
+            "ds_read_u8 %11, %29\n\t"
+            "ds_read_u8 %12, %30\n\t"
+            "ds_read_u8 %13, %31\n\t"
+            "ds_read_u8 %14, %32\n\t"
+            "ds_read_u8 %15, %33\n\t"
+            "ds_read_b64_tr_b8 %16, %34\n\t"
+            "ds_read_b64_tr_b8 %17, %34 offset:%c35\n\t"
+            "s_waitcnt lgkmcnt(0)\n\t"
+            "v_lshl_or_b32 %0, %1, 8, %0\n\t"
+            "v_lshl_or_b32 %2, %3, 8, %2\n\t"
+            "v_lshl_or_b32 %0, %2, 16, %0\n\t"
+            "v_lshl_or_b32 %4, %5, 8, %4\n\t"
+            "v_lshl_or_b32 %6, %7, 8, %6\n\t"
+            "v_lshl_or_b32 %4, %6, 16, %4\n\t"
+            "v_lshl_or_b32 %8, %9, 8, %8\n\t"
+            "v_lshl_or_b32 %10, %11, 8, %10\n\t"
+            "v_lshl_or_b32 %8, %10, 16, %8\n\t"
+            "v_lshl_or_b32 %12, %13, 8, %12\n\t"
+            "v_lshl_or_b32 %14, %15, 8, %14\n\t"
+            "v_lshl_or_b32 %12, %14, 16, %12"
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7]),
+              "=&v"(r[8]), "=&v"(r[9]), "=&v"(r[10]), "=&v"(r[11]), "=&v"(r[12]), "=&v"(r[13]), "=&v"(r[14]),
+              "=&v"(r[15]), "=&v"(t[0]), "=&v"(t[1])
+            : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]), "v"(addr[6]),
+              "v"(addr[7]), "v"(addr[8]), "v"(addr[9]), "v"(addr[10]), "v"(addr[11]), "v"(addr[12]), "v"(addr[13]),
+              "v"(addr[14]), "v"(addr[15]), "v"(base + fr.v[0]), "i"(16 * D));
+    } else if constexpr (D == 64) {
+        asm volatile(
+            "ds_read_u8 %0, %20\n\t"
+            "ds_read_u8 %1, %21\n\t"
+            "ds_read_u8 %2, %22\n\t"
+            "ds_read_u8 %3, %23\n\t"
+            "ds_read_u8 %4, %24\n\t"
+            "ds_read_u8 %5, %25\n\t"
+            "ds_read_u8 %6, %26\n\t"
+            "ds_read_u8 %7, %27\n\t"
+            "ds_read_u8 %8, %28\n\t"
+            "ds_read_u8 %9, %29\n\t"
+            "ds_read_u8 %10, %30\n\t"
+            "ds_read_u8 %11, %31\n\t"
+            "ds_read_u8 %12, %32\n\t"
+            "ds_read_u8 %13, %33\n\t"
+            "ds_read_u8 %14, %34\n\t"
+            "ds_read_u8 %15, %35\n\t"
+            "ds_read_b64_tr_b8 %16, %36\n\t"
+            "ds_read_b64_tr_b8 %17, %36 offset:%c38\n\t"
+            "ds_read_b64_tr_b8 %18, %37\n\t"
+            "ds_read_b64_tr_b8 %19, %37 offset:%c38\n\t"
+            "s_waitcnt lgkmcnt(0)\n\t"
+            "v_lshl_or_b32 %0, %1, 8, %0\n\t"
+            "v_lshl_or_b32 %2, %3, 8, %2\n\t"
+            "v_lshl_or_b32 %0, %2, 16, %0\n\t"
+            "v_lshl_or_b32 %4, %5, 8, %4\n\t"
+            "v_lshl_or_b32 %6, %7, 8, %6\n\t"
+            "v_lshl_or_b32 %4, %6, 16, %4\n\t"
+            "v_lshl_or_b32 %8, %9, 8, %8\n\t"
+            "v_lshl_or_b32 %10, %11, 8, %10\n\t"
+            "v_lshl_or_b32 %8, %10, 16, %8\n\t"
+            "v_lshl_or_b32 %12, %13, 8, %12\n\t"
+            "v_lshl_or_b32 %14, %15, 8, %14\n\t"
+            "v_lshl_or_b32 %12, %14, 16, %12"
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7]),
+              "=&v"(r[8]), "=&v"(r[9]), "=&v"(r[10]), "=&v"(r[11]), "=&v"(r[12]), "=&v"(r[13]), "=&v"(r[14]),
+              "=&v"(r[15]), "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3])
+            : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]), "v"(addr[6]),
+              "v"(addr[7]), "v"(addr[8]), "v"(addr[9]), "v"(addr[10]), "v"(addr[11]), "v"(addr[12]), "v"(addr[13]),
+              "v"(addr[14]), "v"(addr[15]), "v"(base + fr.v[0]), "v"(base + fr.v[1]), "i"(16 * D));
+    } else {
+        asm volatile(
+            "ds_read_u8 %0, %24\n\t"
+            "ds_read_u8 %1, %25\n\t"
+            "ds_read_u8 %2, %26\n\t"
+            "ds_read_u8 %3, %27\n\t"
+            "ds_read_u8 %4, %28\n\t"
+            "ds_read_u8 %5, %29\n\t"
+            "ds_read_u8 %6, %30\n\t"
+            "ds_read_u8 %7, %31\n\t"
+            "ds_read_u8 %8, %32\n\t"
+            "ds_read_u8 %9, %33\n\t"
+            "ds_read_u8 %10, %34\n\t"
+            "ds_read_u8 %11, %35\n\t"
+            "ds_read_u8 %12, %36\n\t"
+            "ds_read_u8 %13, %37\n\t"
+            "ds_read_u8 %14, %38\n\t"
+            "ds_read_u8 %15, %39\n\t"
+            "ds_read_b64_tr_b8 %16, %40\n\t"
+            "ds_read_b64_tr_b8 %17, %40 offset:%c44\n\t"
+            "ds_read_b64_tr_b8 %18, %41\n\t"
+            "ds_read_b64_tr_b8 %19, %41 offset:%c44\n\t"
+            "ds_read_b64_tr_b8 %20, %42\n\t"
+            "ds_read_b64_tr_b8 %21, %42 offset:%c44\n\t"
+            "ds_read_b64_tr_b8 %22, %43\n\t"
+            "ds_read_b64_tr_b8 %23, %43 offset:%c44\n\t"
+            "s_waitcnt lgkmcnt(0)\n\t"
+            "v_lshl_or_b32 %0, %1, 8, %0\n\t"
+            "v_lshl_or_b32 %2, %3, 8, %2\n\t"
+            "v_lshl_or_b32 %0, %2, 16, %0\n\t"
+            "v_lshl_or_b32 %4, %5, 8, %4\n\t"
+            "v_lshl_or_b32 %6, %7, 8, %6\n\t"
+            "v_lshl_or_b32 %4, %6, 16, %4\n\t"
+            "v_lshl_or_b32 %8, %9, 8, %8\n\t"
+            "v_lshl_or_b32 %10, %11, 8, %10\n\t"
+            "v_lshl_or_b32 %8, %10, 16, %8\n\t"
+            "v_lshl_or_b32 %12, %13, 8, %12\n\t"
+            "v_lshl_or_b32 %14, %15, 8, %14\n\t"
+            "v_lshl_or_b32 %12, %14, 16, %12"
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7]),
+              "=&v"(r[8]), "=&v"(r[9]), "=&v"(r[10]), "=&v"(r[11]), "=&v"(r[12]), "=&v"(r[13]), "=&v"(r[14]),
+              "=&v"(r[15]), "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]), "=&v"(t[4]), "=&v"(t[5]), "=&v"(t[6]),
+              "=&v"(t[7])
+            : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]), "v"(addr[6]),
+              "v"(addr[7]), "v"(addr[8]), "v"(addr[9]), "v"(addr[10]), "v"(addr[11]), "v"(addr[12]), "v"(addr[13]),
+              "v"(addr[14]), "v"(addr[15]), "v"(base + fr.v[0]), "v"(base + fr.v[1]), "v"(base + fr.v[2]),
+              "v"(base + fr.v[3]), "i"(16 * D));
+    }
+#pragma unroll
+    for (int w = 0; w < 4; ++w) pk[w] = r[4 * w];
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) vf[i] = i32x4{t[2 * i].x, t[2 * i].y, t[2 * i + 1].x, t[2 * i + 1].y};
+}
+
 // Per-wave state of the fast kernel (S layout for m, l, bnd: lane = query;
 // O layout for acc).
 template <int D>
@@ -607,10 +776,11 @@ __device__ __forceinline__ void load_bias(int32_t* bias_v, const Args& a, const 
 
 // S^T tile of one step with bias and padding applied (kernel.py:153-156, :250-253);
 // returns the row max over the 32 columns (both lane halves).
+// smin: the minimum over the real columns when MASKED or need_min (else INT32_MAX).
 template <int D, bool MASKED, bool TAIL>
 __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& a, const i32x4* qv,
                                           const int8_t* lk, const Frag<D>& fr, const int32_t* bias_v, int kstart,
-                                          int lane) {
+                                          int lane, bool need_min) {
     constexpr int DB = D / 32;
     s = i32x16{};
 #pragma unroll
@@ -624,6 +794,21 @@ __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& 
         for (int v = 0; v < 16; ++v) {
             s[v] = wadd(s[v], bias_v[v]);
             if (!TAIL || kstart + crow(v, lane) < a.N) smin = min(smin, s[v]);
+        }
+    } else if (need_min) {
+        if constexpr (TAIL) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                if (kstart + crow(v, lane) < a.N) smin = min(smin, s[v]);
+        } else {
+            smin = min3(s[0], s[1], s[2]);
+            smin = min3(smin, s[3], s[4]);
+            smin = min3(smin, s[5], s[6]);
+            smin = min3(smin, s[7], s[8]);
+            smin = min3(smin, s[9], s[10]);
+            smin = min3(smin, s[11], s[12]);
+            smin = min3(smin, s[13], s[14]);
+            smin = min(smin, s[15]);
         }
     }
     if constexpr (TAIL) {
@@ -648,7 +833,7 @@ __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& 
 template <int D, bool MASKED, bool TAIL, bool WIDE, bool DYN, bool FIRST>
 __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const i32x4* qv, const int8_t* lk,
                                           const int8_t* lv, const Frag<D>& fr, const BiasRow& brow, int kstart,
-                                          int lane, bool wave_fast, int32_t xlim) {
+                                          int lane, bool wave_fast, int32_t xlim, int lut_mode, uint32_t lut_base) {
     constexpr int DB = D / 32;
     const int g = lane >> 5;
     const int32_t rs = a.rs, eM = a.eM, rM = a.rM;
@@ -657,19 +842,30 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     if constexpr (MASKED) load_bias<TAIL>(bias_v, a, brow, kstart, lane);
     i32x16 s;
     int32_t smin;
-    const int32_t mx = scores<D, MASKED, TAIL>(s, smin, a, qv, lk, fr, bias_v, kstart, lane);
+    const int32_t mx = scores<D, MASKED, TAIL>(s, smin, a, qv, lk, fr, bias_v, kstart, lane, lut_mode == 2);
     const int32_t m = st.m;
     const int32_t mn = max(m, mx);  // kernel.py:158
     const int32_t dm = wsub(m, mn);
     constexpr bool first = FIRST;  // kstart == 0
 
+    if (MASKED || lut_mode == 2) smin = half_min(smin);
+    // table path: every real column of the wave has u = m' - s <= lut_lim
+    // (lut_mode 1: proved for the whole row block from ||q||_1)
+    bool lut_ok = false;
+    if constexpr (!TAIL) lut_ok = lut_mode == 1 || (lut_mode == 2 && __all((int64_t)mn - smin <= a.lut_lim));
     bool vec_ok = wave_fast;
-    if constexpr (MASKED) {
-        smin = half_min(smin);
+    if constexpr (MASKED)
         vec_ok = vec_ok && __all(smin > -(1 << 23) && mn < (1 << 23) && (int64_t)mn - smin <= xlim);
-    }
     uint32_t pk[4];
-    if (vec_ok) {
+    i32x4 vf[DB];
+    if (lut_ok) {
+        // LDS address of entry min(u, lut_n - 1); u <= lut_lim < 2^31 keeps the sum unwrapped
+        const uint32_t cm = (uint32_t)mn + lut_base, cap = lut_base + (uint32_t)(a.lut_n - 1);
+        uint32_t addr[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) addr[v] = min(cm - (uint32_t)s[v], cap);
+        lut_pack_vt<D>(pk, vf, addr, lv, fr);
+    } else if (vec_ok) {
         // kernel.py:159-161 in six ops per score (see the fast-path comment)
         const int32_t c1 = opaque(wadd(wmul(wsub(0, mn), eM), 1 << 16));
         const int32_t c3 = opaque(wsub(rs, mn));
@@ -789,8 +985,7 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     }
     // O += P . V (kernel.py:171)
     const i32x4 pa = i32x4{(int32_t)pk[0], (int32_t)pk[1], (int32_t)pk[2], (int32_t)pk[3]};
-    i32x4 vf[DB];
-    read_vt<D>(vf, lv, fr);
+    if (!lut_ok) read_vt<D>(vf, lv, fr);
 #pragma unroll
     for (int t = 0; t < DB; ++t) st.acc[t] = mfma32(pa, vf[t], st.acc[t]);
     st.m = mn;  // kernel.py:172
@@ -857,9 +1052,10 @@ __device__ __forceinline__ void fast_store(const FastState<D>& st, const Args& a
 template <int D, int W, bool MASKED, bool WIDE, bool DYN>
 __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t* smem, const int8_t* kb,
                                           const int8_t* vb, int z, int h, const BiasRow& brow, int wave, int lane,
-                                          int q0, bool active, bool wave_fast, int32_t xlim) {
+                                          int q0, bool active, bool wave_fast, int32_t xlim, int lut_mode) {
     using S = Stage<D>;
     constexpr int DB = D / 32;
+    const uint32_t lut_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t*)(smem + 2 * S::BYTES);
     FastState<D> st;
 #pragma unroll
     for (int t = 0; t < DB; ++t) st.acc[t] = i32x16{};
@@ -884,7 +1080,7 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
     // carries no first-step cases
     if (active && nfull > 0)
         fast_step<D, MASKED, false, WIDE, DYN, true>(st, a, qv, smem, smem + S::KBYTES, fr, brow, 0, lane, wave_fast,
-                                                     xlim);
+                                                     xlim, lut_mode, lut_base);
     for (int stg = 0; stg < nstage; ++stg) {
         const int8_t* buf = smem + (stg & 1) * S::BYTES;
         if (stg + 1 < nstage) dma.issue(rk, rv, smem + ((stg + 1) & 1) * S::BYTES, (stg + 1) * S::KEYS, a, wave);
@@ -895,7 +1091,7 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
                 if (step >= nfull) break;
                 fast_step<D, MASKED, false, WIDE, DYN, false>(st, a, qv, buf + half * 32 * D,
                                                               buf + S::KBYTES + half * 32 * D, fr, brow, step * 32,
-                                                              lane, wave_fast, xlim);
+                                                              lane, wave_fast, xlim, lut_mode, lut_base);
             }
         }
         stage_sync();
@@ -906,10 +1102,11 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
         const int8_t* lk = buf + th * 32 * D;
         const int8_t* lv = buf + S::KBYTES + th * 32 * D;
         if (nfull == 0)
-            fast_step<D, MASKED, true, WIDE, DYN, true>(st, a, qv, lk, lv, fr, brow, 0, lane, wave_fast, xlim);
+            fast_step<D, MASKED, true, WIDE, DYN, true>(st, a, qv, lk, lv, fr, brow, 0, lane, wave_fast, xlim, 0,
+                                                        lut_base);
         else
             fast_step<D, MASKED, true, WIDE, DYN, false>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane, wave_fast,
-                                                         xlim);
+                                                         xlim, 0, lut_base);
     }
     if (!active) return;
     fast_store<D>(st, a, z, h, lane, q0);
@@ -924,9 +1121,11 @@ template <int D, int W, bool MASKED, bool DYN>
 __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Args a) {
     using S = Stage<D>;
     constexpr int DB = D / 32;
-    __shared__ __attribute__((aligned(16))) int8_t smem[2 * S::BYTES];
+    __shared__ __attribute__((aligned(16))) int8_t smem[2 * S::BYTES + kLutMax];
 
     const int tid = threadIdx.x;
+    // p(u) table (lut_pack_vt), visible after fast_rows' first barrier
+    for (int u = tid; u < a.lut_n; u += 64 * W) smem[2 * S::BYTES + u] = (int8_t)requant(exp2_i32(-u, a), a);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int lq = lane & 31, g = lane >> 5;
     const int wg = xcd_order(blockIdx.x, a.n_wg);
@@ -966,6 +1165,7 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
     // per step.
     bool wave_fast = !a.force_robust;
     int32_t xlim = a.x_safe;
+    int lut_mode = a.lut_n ? 2 : 0;  // 1: u <= lut_lim for every real column, 2: checked per step
     if constexpr (!MASKED) {
         // sum |q|: bytes offset by 128 (xor 0x80) against 0x80 under v_sad_u8
         uint32_t l1u = 0;
@@ -982,6 +1182,7 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
                         ((X * a.eps_abs + 65535) >> 16) + 2 * (int64_t)a.rs + 1 < (1 << 22);
         wave_fast = wave_fast && __all(ok);
         xlim = (int32_t)(X < (1 << 30) ? X : (1 << 30));
+        if (a.lut_n) lut_mode = __all(X <= a.lut_lim) ? 1 : 2;
     }
 
     // Unmasked waves whose guard holds run a loop that never meets an alpha
@@ -990,11 +1191,14 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
     // writes its own rows, so the two never merge register state.
     if constexpr (!MASKED) {
         if (wave_fast)
-            fast_rows<D, W, false, false, DYN>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active, wave_fast, xlim);
+            fast_rows<D, W, false, false, DYN>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active, wave_fast, xlim,
+                                               lut_mode);
         else
-            fast_rows<D, W, false, true, DYN>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active, wave_fast, xlim);
+            fast_rows<D, W, false, true, DYN>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active, wave_fast, xlim,
+                                               lut_mode);
     } else {
-        fast_rows<D, W, true, true, DYN>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active, wave_fast, xlim);
+        fast_rows<D, W, true, true, DYN>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active, wave_fast, xlim,
+                                               lut_mode);
     }
 }
 
@@ -1095,6 +1299,53 @@ static hipError_t launch_d(const Args& a, int W, bool vec, bool fast, dim3 grid,
     }
 }
 
+static bool getenv_flag(const char* name);
+
+// Bounds of the fast kernel's exp2 + requantisation table (see lut_pack_vt):
+// n entries p(0 .. n - 1), the last one 0, and lim such that p(u) = 0 for
+// every u in [n - 1, lim].  From u0 on (q >= bitlen(rs) + 3) the bound of
+// lut_pack_vt's comment gives E = 0 up to lim; below u0 the values are
+// computed here, with the kernel's own integer primitives.  n = 0: no table.
+static void lut_bounds(const Args& a, int32_t* n_out, int32_t* lim_out) {
+    *n_out = 0;
+    *lim_out = 0;
+    const int64_t A = -(int64_t)a.eM, rs = a.rs;
+    if (!a.exp_mode || A <= 0 || rs <= 0) return;
+    const int64_t kap = A * rs - 65536;
+    if (kap > 2 * A) return;
+    int64_t lim = (int64_t)INT32_MAX / A;              // u * |eM| < 2^31: x * eM does not wrap
+    if (kap < 0 && rs * 65536 / -kap < lim) lim = rs * 65536 / -kap;  // r >= -2 rs
+    int bl = 0;
+    while ((1ll << bl) <= rs) ++bl;
+    const int64_t u0 = ((bl + 3) * 65536 + A - 1) / A;  // q >= bitlen(rs) + 3 for u >= u0
+    if (u0 > lim || u0 >= kLutMax) return;
+    int64_t n = 1;
+    for (int64_t u = u0; u >= 0; --u)
+        if (requant(exp2_i32((int32_t)-u, a), a) != 0) {
+            n = u + 2;
+            break;
+        }
+    *n_out = (int32_t)n;
+    *lim_out = (int32_t)lim;
+}
+
+// The table for this call, or none (lut_n = 0).  Filling it costs each
+// workgroup a few hundred VALU operations and every step an LDS round trip,
+// so it is used for rows of at least 4 steps in grids of at least two rounds
+// of waves (measured on MI355X: 8% slower at ViT-S 197 x 64 x 6 heads x 64,
+// one round; 9% faster at ViT-B/384, 3.75 rounds).
+static void choose_lut(Args& a, int W) {
+    a.lut_n = 0;
+    a.lut_lim = 0;
+    if (a.force_robust || getenv_flag("QFLASH_HIP_NO_LUT")) return;  // test hooks
+    const bool pays = a.N >= 128 && (int64_t)a.n_wg * W >= 8192;
+    if (!pays && !getenv_flag("QFLASH_HIP_FORCE_LUT")) return;
+    int32_t n, lim;
+    lut_bounds(a, &n, &lim);
+    a.lut_n = n;
+    a.lut_lim = lim;
+}
+
 // Proof obligations of fwd_fast (see the comment above it).  Returns true and
 // fills a.x_safe / a.id_ok when the fast path computes exactly what the
 // reference does for every possible int8 input of this shape.
@@ -1172,7 +1423,7 @@ static int forward(const int8_t* Q, const int8_t* K, const int8_t* V, void* O, c
         INT32_MAX)
         return fail(QFLASH_HIP_EINVAL, "one head's output spans more than 2 GiB");
 
-    Args a;
+    Args a{};
     a.q = Q; a.k = K; a.v = V; a.bias = bias;
     a.o = out_dt == QFLASH_HIP_I8 ? (int8_t*)O : nullptr;
     a.out_t = out_dt == QFLASH_HIP_I8 ? nullptr : O;
@@ -1214,9 +1465,12 @@ static int forward(const int8_t* Q, const int8_t* K, const int8_t* V, void* O, c
     // Test hooks (environment, read per call): QFLASH_HIP_FORCE_GENERAL selects the
     // general kernel; QFLASH_HIP_FORCE_DYNAMIC_BOUND / QFLASH_HIP_FORCE_ROBUST drive the
     // fast kernel's exact fallbacks on inputs that would not need them.
-    const bool fast = choose_fast(a, D, masked, vec) && !getenv_flag("QFLASH_HIP_FORCE_GENERAL");
-    if (getenv_flag("QFLASH_HIP_FORCE_DYNAMIC_BOUND")) a.id_ok = 0;
+    // QFLASH_HIP_NO_LUT / QFLASH_HIP_FORCE_LUT turn the fast kernel's table path
+    // off / on whatever the shape.
     a.force_robust = getenv_flag("QFLASH_HIP_FORCE_ROBUST") ? 1 : 0;
+    const bool fast = choose_fast(a, D, masked, vec) && !getenv_flag("QFLASH_HIP_FORCE_GENERAL");
+    if (fast) choose_lut(a, W);
+    if (getenv_flag("QFLASH_HIP_FORCE_DYNAMIC_BOUND")) a.id_ok = 0;
     dim3 grid((unsigned)nwg);
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;
@@ -1286,6 +1540,18 @@ int qflash_hip_mfma_layout_check(const int8_t* A, const int8_t* B, int32_t* C, v
     hipLaunchKernelGGL(qf::mfma_layout_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, A, B, C);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return qf::fail(QFLASH_HIP_ELAUNCH, "launch failed: %s", hipGetErrorString(e));
+    return QFLASH_HIP_OK;
+}
+
+int qflash_hip_lut_bounds(int32_t sm_rscale, int32_t exp_M, int32_t req_M, int32_t* lut_n, int32_t* lut_lim) {
+    qferr::g_err[0] = 0;
+    if (!lut_n || !lut_lim) return qferr::fail(QFLASH_HIP_EINVAL, "null pointer argument");
+    qf::Args a{};
+    a.rs = sm_rscale;
+    a.eM = exp_M;
+    a.rM = req_M;
+    a.exp_mode = 1;
+    qf::lut_bounds(a, lut_n, lut_lim);
     return QFLASH_HIP_OK;
 }
 

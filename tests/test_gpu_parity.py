@@ -76,7 +76,8 @@ def test_golden_codes(name):
     np.testing.assert_array_equal(o.cpu().numpy(), c["o_i8"])
 
 
-HOOKS = ["QFLASH_HIP_FORCE_GENERAL", "QFLASH_HIP_FORCE_DYNAMIC_BOUND", "QFLASH_HIP_FORCE_ROBUST"]
+HOOKS = ["QFLASH_HIP_FORCE_GENERAL", "QFLASH_HIP_FORCE_DYNAMIC_BOUND", "QFLASH_HIP_FORCE_ROBUST", "QFLASH_HIP_NO_LUT",
+         "QFLASH_HIP_FORCE_LUT"]
 
 
 @pytest.mark.parametrize("hook", HOOKS)
@@ -84,8 +85,9 @@ HOOKS = ["QFLASH_HIP_FORCE_GENERAL", "QFLASH_HIP_FORCE_DYNAMIC_BOUND", "QFLASH_H
 def test_golden_codes_forced_paths(name, hook, monkeypatch):
     """Every exact fallback on every case: the general kernel (used when the fast
     path's constant guards fail), the fast kernel's per-row dynamic bound for the
-    identity rescale, and its robust continuation (general arithmetic, used
-    when a per-wave or per-step guard fails)."""
+    identity rescale, its robust continuation (general arithmetic, used when a
+    per-wave or per-step guard fails), and its arithmetic and table exp2 paths
+    (the table off / on whatever the launch size)."""
     monkeypatch.setenv(hook, "1")
     test_golden_codes(name)
 
@@ -198,3 +200,37 @@ def test_adversarial_int8_inputs(pattern, D, sm_scale):
     torch.cuda.synchronize()
     got = o.cpu().numpy()
     assert int((got != want).sum()) == 0
+
+
+@pytest.mark.parametrize("masked", [False, True])
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("sm_scale", [1 / 3.4, 1 / 2.6, 1 / 57.3, 1 / 94.2, 0.0123])
+def test_table_path_vs_oracle(sm_scale, D, masked, monkeypatch):
+    """The exp2 table of the fast kernel under scales with both signs of
+    kappa: with small zero ranges (1/3.4: lut_lim = 25) most steps fail the
+    per-step check and mix with the arithmetic path; rows of growing spread
+    reach every case."""
+    import ctypes
+    monkeypatch.setenv("QFLASH_HIP_FORCE_LUT", "1")
+    from qflash_amd.kernel import fixed_point_constants, mask_to_bias
+    consts = Consts(*fixed_point_constants(sm_scale, 30, 30))
+    n, lim = ctypes.c_int32(), ctypes.c_int32()
+    _lib().load().qflash_hip_lut_bounds(consts.sm_rscale, consts.exp_M, consts.req_M, ctypes.byref(n),
+                                        ctypes.byref(lim))
+    print(f"[case] sm_scale={sm_scale} D={D} masked={masked} consts={consts} lut=({n.value}, {lim.value})",
+          flush=True)
+    assert n.value > 0
+    g = np.random.default_rng(D + int(1e4 * sm_scale) + masked)
+    N = 200
+    spread = np.linspace(1, 40, N)[None, None, :, None]
+    q8, k8, v8 = (torch.from_numpy(np.clip(np.rint(g.standard_normal((2, 2, N, D)) * s), -128, 127).astype(np.int8))
+                  for s in (spread, np.full_like(spread, 6.0), np.full_like(spread, 50.0)))
+    bias = None
+    if masked:
+        bias = mask_to_bias(torch.from_numpy(g.random((N, N)) > 0.1), sm_scale, 2, 2, N)
+    want = oracle_c.attention_codes(q8, k8, v8, consts, Flags(), bias=bias, threads=8)
+    qd, kd, vd = q8.to(DEV), k8.to(DEV), v8.to(DEV)
+    o = torch.empty_like(vd)
+    _launch(qd, kd, vd, o, consts, Flags(), None if bias is None else bias.to(DEV))
+    torch.cuda.synchronize()
+    assert int((o.cpu().numpy() != want).sum()) == 0
