@@ -24,6 +24,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <atomic>
+#include <utility>
 #include <stdint.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -43,7 +44,7 @@ constexpr int32_t kNegInf = -(1 << 20);  // kernel.py:137
 #define QF_FAST_WAVES_D64 4
 #endif
 constexpr int kBN = 32;                   // kernel.py:27, one rescale step
-constexpr int kLutMax = 8192;             // bytes of LDS for the p(u) table of the fast kernel
+constexpr int kLutMax = 4096;             // bytes of LDS for the p(u) table of the fast kernel
 
 struct Args {
     const int8_t* q;
@@ -173,6 +174,10 @@ __device__ __forceinline__ i32x16 mfma32(i32x4 a, i32x4 b, i32x16 c) {
 
 // Row (within a 32-row block) held by result register v of lane l.
 __device__ __forceinline__ int crow(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
+// Key column kstart + crow(v, lane) lies past N (a padded column of the last
+// step) iff 8*(v>>2) + (v&3) >= tcut, tcut = N - kstart - 4*(lane>>5): one
+// per-lane value and compile-time constants, instead of 16 column indices.
+__device__ __forceinline__ bool padded(int v, int32_t tcut) { return 8 * (v >> 2) + (v & 3) >= tcut; }
 
 // 16 bytes from global memory; `vec` = base 16-byte aligned and unit stride.
 template <bool VEC>
@@ -556,6 +561,15 @@ __device__ __forceinline__ int32_t half_min(int32_t v) {
     const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
     return min((int32_t)r[0], (int32_t)r[1]);
 }
+// ds_bpermute_b32 with the lane's byte address split into a register and an
+// immediate offset: through the builtin the compiler hoists the 16 distinct
+// addresses of the rescale out of the loop and holds 16 VGPRs for them.
+template <int OFF>
+__device__ __forceinline__ int32_t bpermute_off(int32_t addr, int32_t v) {
+    int32_t r;
+    asm volatile("ds_bpermute_b32 %0, %1, %2 offset:%3\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr), "v"(v), "i"(OFF));
+    return r;
+}
 // Keeps the compiler from distributing a per-row constant back into the
 // per-element expressions (it would turn one mad into mul + sub + add).
 __device__ __forceinline__ int32_t opaque(int32_t v) {
@@ -598,28 +612,31 @@ __device__ __forceinline__ void lut_pack_vt(uint32_t* pk, i32x4* vf, const uint3
                                             const Frag<D>& fr) {
     typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
     const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)lv;
+    // each byte load writes its result over its own address register
     uint32_t r[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) r[i] = addr[i];
     i32x2 t[2 * (D / 32)];
     if constexpr (D == 32) {
         asm volatile(
-            "ds_read_u8 %0, %18\n\t"
-            "ds_read_u8 %1, %19\n\t"
-            "ds_read_u8 %2, %20\n\t"
-            "ds_read_u8 %3, %21\n\t"
-            "ds_read_u8 %4, %22\n\t"
-            "ds_read_u8 %5, %23\n\t"
-            "ds_read_u8 %6, %24\n\t"
-            "ds_read_u8 %7, %25\n\t"
-            "ds_read_u8 %8, %26\n\t"
-            "ds_read_u8 %9, %27\n\t"
-            "ds_read_u8 %10, %28\n\t"
-            "ds_read_u8 %11, %29\n\t"
-            "ds_read_u8 %12, %30\n\t"
-            "ds_read_u8 %13, %31\n\t"
-            "ds_read_u8 %14, %32\n\t"
-            "ds_read_u8 %15, %33\n\t"
-            "ds_read_b64_tr_b8 %16, %34\n\t"
-            "ds_read_b64_tr_b8 %17, %34 offset:%c35\n\t"
+            "ds_read_u8 %0, %0\n\t"
+            "ds_read_u8 %1, %1\n\t"
+            "ds_read_u8 %2, %2\n\t"
+            "ds_read_u8 %3, %3\n\t"
+            "ds_read_u8 %4, %4\n\t"
+            "ds_read_u8 %5, %5\n\t"
+            "ds_read_u8 %6, %6\n\t"
+            "ds_read_u8 %7, %7\n\t"
+            "ds_read_u8 %8, %8\n\t"
+            "ds_read_u8 %9, %9\n\t"
+            "ds_read_u8 %10, %10\n\t"
+            "ds_read_u8 %11, %11\n\t"
+            "ds_read_u8 %12, %12\n\t"
+            "ds_read_u8 %13, %13\n\t"
+            "ds_read_u8 %14, %14\n\t"
+            "ds_read_u8 %15, %15\n\t"
+            "ds_read_b64_tr_b8 %16, %18\n\t"
+            "ds_read_b64_tr_b8 %17, %18 offset:%c19\n\t"
             "s_waitcnt lgkmcnt(0)\n\t"
             "v_lshl_or_b32 %0, %1, 8, %0\n\t"
             "v_lshl_or_b32 %2, %3, 8, %2\n\t"
@@ -633,34 +650,32 @@ __device__ __forceinline__ void lut_pack_vt(uint32_t* pk, i32x4* vf, const uint3
             "v_lshl_or_b32 %12, %13, 8, %12\n\t"
             "v_lshl_or_b32 %14, %15, 8, %14\n\t"
             "v_lshl_or_b32 %12, %14, 16, %12"
-            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7]),
-              "=&v"(r[8]), "=&v"(r[9]), "=&v"(r[10]), "=&v"(r[11]), "=&v"(r[12]), "=&v"(r[13]), "=&v"(r[14]),
-              "=&v"(r[15]), "=&v"(t[0]), "=&v"(t[1])
-            : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]), "v"(addr[6]),
-              "v"(addr[7]), "v"(addr[8]), "v"(addr[9]), "v"(addr[10]), "v"(addr[11]), "v"(addr[12]), "v"(addr[13]),
-              "v"(addr[14]), "v"(addr[15]), "v"(base + fr.v[0]), "i"(16 * D));
+            : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),
+              "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]), "+v"(r[12]), "+v"(r[13]), "+v"(r[14]), "+v"(r[15]),
+              "=&v"(t[0]), "=&v"(t[1])
+            : "v"(base + fr.v[0]), "i"(16 * D));
     } else if constexpr (D == 64) {
         asm volatile(
-            "ds_read_u8 %0, %20\n\t"
-            "ds_read_u8 %1, %21\n\t"
-            "ds_read_u8 %2, %22\n\t"
-            "ds_read_u8 %3, %23\n\t"
-            "ds_read_u8 %4, %24\n\t"
-            "ds_read_u8 %5, %25\n\t"
-            "ds_read_u8 %6, %26\n\t"
-            "ds_read_u8 %7, %27\n\t"
-            "ds_read_u8 %8, %28\n\t"
-            "ds_read_u8 %9, %29\n\t"
-            "ds_read_u8 %10, %30\n\t"
-            "ds_read_u8 %11, %31\n\t"
-            "ds_read_u8 %12, %32\n\t"
-            "ds_read_u8 %13, %33\n\t"
-            "ds_read_u8 %14, %34\n\t"
-            "ds_read_u8 %15, %35\n\t"
-            "ds_read_b64_tr_b8 %16, %36\n\t"
-            "ds_read_b64_tr_b8 %17, %36 offset:%c38\n\t"
-            "ds_read_b64_tr_b8 %18, %37\n\t"
-            "ds_read_b64_tr_b8 %19, %37 offset:%c38\n\t"
+            "ds_read_u8 %0, %0\n\t"
+            "ds_read_u8 %1, %1\n\t"
+            "ds_read_u8 %2, %2\n\t"
+            "ds_read_u8 %3, %3\n\t"
+            "ds_read_u8 %4, %4\n\t"
+            "ds_read_u8 %5, %5\n\t"
+            "ds_read_u8 %6, %6\n\t"
+            "ds_read_u8 %7, %7\n\t"
+            "ds_read_u8 %8, %8\n\t"
+            "ds_read_u8 %9, %9\n\t"
+            "ds_read_u8 %10, %10\n\t"
+            "ds_read_u8 %11, %11\n\t"
+            "ds_read_u8 %12, %12\n\t"
+            "ds_read_u8 %13, %13\n\t"
+            "ds_read_u8 %14, %14\n\t"
+            "ds_read_u8 %15, %15\n\t"
+            "ds_read_b64_tr_b8 %16, %20\n\t"
+            "ds_read_b64_tr_b8 %17, %20 offset:%c22\n\t"
+            "ds_read_b64_tr_b8 %18, %21\n\t"
+            "ds_read_b64_tr_b8 %19, %21 offset:%c22\n\t"
             "s_waitcnt lgkmcnt(0)\n\t"
             "v_lshl_or_b32 %0, %1, 8, %0\n\t"
             "v_lshl_or_b32 %2, %3, 8, %2\n\t"
@@ -674,38 +689,36 @@ __device__ __forceinline__ void lut_pack_vt(uint32_t* pk, i32x4* vf, const uint3
             "v_lshl_or_b32 %12, %13, 8, %12\n\t"
             "v_lshl_or_b32 %14, %15, 8, %14\n\t"
             "v_lshl_or_b32 %12, %14, 16, %12"
-            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7]),
-              "=&v"(r[8]), "=&v"(r[9]), "=&v"(r[10]), "=&v"(r[11]), "=&v"(r[12]), "=&v"(r[13]), "=&v"(r[14]),
-              "=&v"(r[15]), "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3])
-            : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]), "v"(addr[6]),
-              "v"(addr[7]), "v"(addr[8]), "v"(addr[9]), "v"(addr[10]), "v"(addr[11]), "v"(addr[12]), "v"(addr[13]),
-              "v"(addr[14]), "v"(addr[15]), "v"(base + fr.v[0]), "v"(base + fr.v[1]), "i"(16 * D));
+            : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),
+              "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]), "+v"(r[12]), "+v"(r[13]), "+v"(r[14]), "+v"(r[15]),
+              "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3])
+            : "v"(base + fr.v[0]), "v"(base + fr.v[1]), "i"(16 * D));
     } else {
         asm volatile(
-            "ds_read_u8 %0, %24\n\t"
-            "ds_read_u8 %1, %25\n\t"
-            "ds_read_u8 %2, %26\n\t"
-            "ds_read_u8 %3, %27\n\t"
-            "ds_read_u8 %4, %28\n\t"
-            "ds_read_u8 %5, %29\n\t"
-            "ds_read_u8 %6, %30\n\t"
-            "ds_read_u8 %7, %31\n\t"
-            "ds_read_u8 %8, %32\n\t"
-            "ds_read_u8 %9, %33\n\t"
-            "ds_read_u8 %10, %34\n\t"
-            "ds_read_u8 %11, %35\n\t"
-            "ds_read_u8 %12, %36\n\t"
-            "ds_read_u8 %13, %37\n\t"
-            "ds_read_u8 %14, %38\n\t"
-            "ds_read_u8 %15, %39\n\t"
-            "ds_read_b64_tr_b8 %16, %40\n\t"
-            "ds_read_b64_tr_b8 %17, %40 offset:%c44\n\t"
-            "ds_read_b64_tr_b8 %18, %41\n\t"
-            "ds_read_b64_tr_b8 %19, %41 offset:%c44\n\t"
-            "ds_read_b64_tr_b8 %20, %42\n\t"
-            "ds_read_b64_tr_b8 %21, %42 offset:%c44\n\t"
-            "ds_read_b64_tr_b8 %22, %43\n\t"
-            "ds_read_b64_tr_b8 %23, %43 offset:%c44\n\t"
+            "ds_read_u8 %0, %0\n\t"
+            "ds_read_u8 %1, %1\n\t"
+            "ds_read_u8 %2, %2\n\t"
+            "ds_read_u8 %3, %3\n\t"
+            "ds_read_u8 %4, %4\n\t"
+            "ds_read_u8 %5, %5\n\t"
+            "ds_read_u8 %6, %6\n\t"
+            "ds_read_u8 %7, %7\n\t"
+            "ds_read_u8 %8, %8\n\t"
+            "ds_read_u8 %9, %9\n\t"
+            "ds_read_u8 %10, %10\n\t"
+            "ds_read_u8 %11, %11\n\t"
+            "ds_read_u8 %12, %12\n\t"
+            "ds_read_u8 %13, %13\n\t"
+            "ds_read_u8 %14, %14\n\t"
+            "ds_read_u8 %15, %15\n\t"
+            "ds_read_b64_tr_b8 %16, %24\n\t"
+            "ds_read_b64_tr_b8 %17, %24 offset:%c28\n\t"
+            "ds_read_b64_tr_b8 %18, %25\n\t"
+            "ds_read_b64_tr_b8 %19, %25 offset:%c28\n\t"
+            "ds_read_b64_tr_b8 %20, %26\n\t"
+            "ds_read_b64_tr_b8 %21, %26 offset:%c28\n\t"
+            "ds_read_b64_tr_b8 %22, %27\n\t"
+            "ds_read_b64_tr_b8 %23, %27 offset:%c28\n\t"
             "s_waitcnt lgkmcnt(0)\n\t"
             "v_lshl_or_b32 %0, %1, 8, %0\n\t"
             "v_lshl_or_b32 %2, %3, 8, %2\n\t"
@@ -719,14 +732,10 @@ __device__ __forceinline__ void lut_pack_vt(uint32_t* pk, i32x4* vf, const uint3
             "v_lshl_or_b32 %12, %13, 8, %12\n\t"
             "v_lshl_or_b32 %14, %15, 8, %14\n\t"
             "v_lshl_or_b32 %12, %14, 16, %12"
-            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7]),
-              "=&v"(r[8]), "=&v"(r[9]), "=&v"(r[10]), "=&v"(r[11]), "=&v"(r[12]), "=&v"(r[13]), "=&v"(r[14]),
-              "=&v"(r[15]), "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]), "=&v"(t[4]), "=&v"(t[5]), "=&v"(t[6]),
-              "=&v"(t[7])
-            : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]), "v"(addr[6]),
-              "v"(addr[7]), "v"(addr[8]), "v"(addr[9]), "v"(addr[10]), "v"(addr[11]), "v"(addr[12]), "v"(addr[13]),
-              "v"(addr[14]), "v"(addr[15]), "v"(base + fr.v[0]), "v"(base + fr.v[1]), "v"(base + fr.v[2]),
-              "v"(base + fr.v[3]), "i"(16 * D));
+            : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),
+              "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]), "+v"(r[12]), "+v"(r[13]), "+v"(r[14]), "+v"(r[15]),
+              "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]), "=&v"(t[4]), "=&v"(t[5]), "=&v"(t[6]), "=&v"(t[7])
+            : "v"(base + fr.v[0]), "v"(base + fr.v[1]), "v"(base + fr.v[2]), "v"(base + fr.v[3]), "i"(16 * D));
     }
 #pragma unroll
     for (int w = 0; w < 4; ++w) pk[w] = r[4 * w];
@@ -789,17 +798,18 @@ __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& 
         s = mfma32(kf, qv[db], s);
     }
     smin = INT32_MAX;
+    const int32_t tcut = a.N - kstart - 4 * (lane >> 5);
     if constexpr (MASKED) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             s[v] = wadd(s[v], bias_v[v]);
-            if (!TAIL || kstart + crow(v, lane) < a.N) smin = min(smin, s[v]);
+            if (!TAIL || !padded(v, tcut)) smin = min(smin, s[v]);
         }
     } else if (need_min) {
         if constexpr (TAIL) {
 #pragma unroll
             for (int v = 0; v < 16; ++v)
-                if (kstart + crow(v, lane) < a.N) smin = min(smin, s[v]);
+                if (!padded(v, tcut)) smin = min(smin, s[v]);
         } else {
             smin = min3(s[0], s[1], s[2]);
             smin = min3(smin, s[3], s[4]);
@@ -814,7 +824,7 @@ __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& 
     if constexpr (TAIL) {
 #pragma unroll
         for (int v = 0; v < 16; ++v)
-            if (kstart + crow(v, lane) >= a.N) s[v] = kNegInf;
+            if (padded(v, tcut)) s[v] = kNegInf;
     }
     int32_t mx = max3(s[0], s[1], s[2]);
     mx = max3(mx, s[3], s[4]);
@@ -880,9 +890,10 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
         }
         if constexpr (TAIL) {  // padded key columns: p(NEG_INF - m') exactly, once per row
             const int32_t ppad = (int32_t)((uint32_t)requant(exp2_i32(wsub(kNegInf, mn), a), a) << 16);
+            const int32_t tcut = a.N - kstart - 4 * g;
 #pragma unroll
             for (int v = 0; v < 16; ++v)
-                if (kstart + crow(v, lane) >= a.N) s[v] = ppad;
+                if (padded(v, tcut)) s[v] = ppad;
         }
 #pragma unroll
         for (int w4 = 0; w4 < 4; ++w4) {
@@ -890,16 +901,21 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
             const uint32_t hi = __builtin_amdgcn_perm((uint32_t)s[4 * w4 + 3], (uint32_t)s[4 * w4 + 2], 0x0c0c0602u);
             pk[w4] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
         }
-    } else {  // general exact arithmetic for this step's scores
+    } else {  // general exact arithmetic for this step's scores (p in bits 0-7)
+        // One score at a time through a rotating queue: this rare path then holds
+        // the temporaries of one evaluation only, not of sixteen interleaved ones.
+#pragma unroll 1
+        for (int i = 0; i < 16; ++i) {
+            const int32_t pv = requant(exp2_i32(wsub(s[0], mn), a), a);
+#pragma unroll
+            for (int v = 0; v < 15; ++v) s[v] = s[v + 1];
+            s[15] = pv;
+        }
 #pragma unroll
         for (int w4 = 0; w4 < 4; ++w4) {
-            uint32_t wv = 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int32_t p = requant(exp2_i32(wsub(s[4 * w4 + e], mn), a), a);
-                wv |= ((uint32_t)p & 0xffu) << (8 * e);
-            }
-            pk[w4] = wv;
+            const uint32_t lo = __builtin_amdgcn_perm((uint32_t)s[4 * w4 + 1], (uint32_t)s[4 * w4], 0x0c0c0400u);
+            const uint32_t hi = __builtin_amdgcn_perm((uint32_t)s[4 * w4 + 3], (uint32_t)s[4 * w4 + 2], 0x0c0c0400u);
+            pk[w4] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
         }
     }
     // kernel.py:162
@@ -956,23 +972,26 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
             // acc*A64 + 2^(as-1) mod 2^64 = acc*sext(A) + 2^(as-1) + (acc*Ah << 32)
             const int64_t ahalf = 1ll << (as - 1);
             const int addr = g * 16;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int rlo = 8 * (v >> 2) + (v & 3);
-                if (chg & ((1u << rlo) | (1u << (rlo + 4)))) {
-                    const int32_t av = __builtin_amdgcn_ds_bpermute(addr + 4 * rlo, A);
+            // bit rlo: row rlo or rlo + 4 changed (one scalar bit test per pair)
+            const uint32_t pairs = (chg | (chg >> 4)) & 0x0F0F0F0Fu;
+            auto pair = [&]<int V>() {
+                constexpr int rlo = 8 * (V >> 2) + (V & 3);
+                if ((pairs >> rlo) & 1u) {
+                    const int32_t av = bpermute_off<4 * rlo>(addr, A);
                     int32_t ah = 0;
-                    if constexpr (WIDE) ah = wide ? __builtin_amdgcn_ds_bpermute(addr + 4 * rlo, Ah) : 0;
+                    if constexpr (WIDE) ah = wide ? bpermute_off<4 * rlo>(addr, Ah) : 0;
 #pragma unroll
                     for (int t = 0; t < DB; ++t) {
-                        const int64_t p = (int64_t)st.acc[t][v] * (int64_t)av + ahalf;
+                        const int64_t p = (int64_t)st.acc[t][V] * (int64_t)av + ahalf;
                         uint32_t hi = (uint32_t)(p >> 32);
                         if constexpr (WIDE)
-                            if (wide) hi += (uint32_t)wmul(st.acc[t][v], ah);
-                        st.acc[t][v] = (int32_t)__builtin_amdgcn_alignbit(hi, (uint32_t)p, (uint32_t)as);
+                            if (wide) hi += (uint32_t)wmul(st.acc[t][V], ah);
+                        st.acc[t][V] = (int32_t)__builtin_amdgcn_alignbit(hi, (uint32_t)p, (uint32_t)as);
                     }
                 }
-            }
+            };
+            [&]<int... V>(std::integer_sequence<int, V...>) { (pair.template operator()<V>(), ...); }(
+                std::make_integer_sequence<int, 16>{});
         }
     }
     if constexpr (DYN) {  // |P.V| <= 128 * sum|p|, and sum|p| <= sum of the bytes read as unsigned

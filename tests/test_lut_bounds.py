@@ -20,7 +20,7 @@ from oracle.qflash_oracle import Consts, exp2_i32, requantize
 from qflash_amd import _build, _lib
 from qflash_amd.kernel import fixed_point_constants
 
-KLUT_MAX = 8192          # bytes of LDS the kernel reserves for the table
+KLUT_MAX = 4096          # bytes of LDS the kernel reserves for the table
 BRUTE_CAP = 1 << 22      # brute-force range per constant set
 
 
