@@ -41,7 +41,7 @@ extern "C" {
 #define QFLASH_HIP_F16 1
 #define QFLASH_HIP_BF16 2
 #define QFLASH_HIP_I8 3 /* output: the int8 codes themselves */
-#define QFLASH_HIP_SCALES_WORKSPACE 192
+#define QFLASH_HIP_SCALES_WORKSPACE 256
 
 /* Arithmetic-variant switches, kernel.py:30-36 (QFLASH_* environment). */
 typedef struct qflash_hip_flags {
@@ -100,9 +100,11 @@ int qflash_hip_window_kernel(const int8_t* Q, const int8_t* K, const int8_t* V, 
  *                  to the dtype (torch's division of a device tensor by a host
  *                  scalar), scales[3] = scales[0] * scales[1] rounded to the dtype.
  * shapes_strides: for q, k, v in turn, 4 sizes (Z, H, N, D) then 4 element strides.
- * workspace: at least QFLASH_HIP_SCALES_WORKSPACE device uint32 entries,
- * ZERO-INITIALISED by the caller (partial maxima are accumulated there with
- * atomic max; the call allocates nothing).
+ * workspace: at least QFLASH_HIP_SCALES_WORKSPACE device uint32 entries, all
+ * ZERO before the first call (partial maxima are kept there); each call
+ * leaves them zero again when it completes, so one workspace serves any
+ * number of calls in stream order.  Calls that share a workspace must not
+ * overlap.  The call allocates nothing.
  */
 int qflash_hip_scales(const void* q, const void* k, const void* v, int32_t dtype, const int64_t* shapes_strides,
                       void* scales, uint32_t* workspace, int64_t workspace_elems, void* stream);

@@ -37,7 +37,7 @@ EXPORTS = ("qflash_hip_kernel", "qflash_hip_masked_kernel", "qflash_hip_window_k
 
 # element type codes of qflash_hip_scales / qflash_hip_quantize, and its workspace
 F32, F16, BF16, I8 = 0, 1, 2, 3
-SCALES_WORKSPACE = 192
+SCALES_WORKSPACE = 256
 
 E_HEADDIM = -2
 

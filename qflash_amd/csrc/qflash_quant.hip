@@ -6,9 +6,9 @@
 //     x_scale = x.abs().amax() / 127                  (in the input dtype T)
 //     qk      = q_scale * k_scale                     (in T; .item() on the host)
 //     x_i8    = clamp(round(x / x_scale), -128, 127).to(int8)
-// Here: one pass reads each input once for the absmax (qflash_hip_scales), a
-// one-thread pass forms the scales in T, and one pass reads each input again
-// and writes the int8 codes (qflash_hip_quantize).  The arithmetic is torch's
+// Here: one pass reads each input once for the absmax, a one-wave pass forms
+// the scales in T (qflash_hip_scales), and one pass reads each input again and
+// writes the int8 codes (qflash_hip_quantize).  The arithmetic is torch's
 // on the GPU for T: fp32 natively; fp16 / bf16 as fp32 opmath rounded back to
 // T after every operation; a division by the host scalar 127 is a product
 // with RN_fp32(1/127); round half to even; clamp; conversion.
@@ -33,9 +33,13 @@ namespace qfq {
 using qferr::fail;
 using qferr::g_err;
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
 constexpr int kThreads = 256;
 constexpr int kSeg = 8 * kThreads;  // 16-byte chunks per work unit
 constexpr int kSlots = 64;          // atomic-max slots per tensor (spreads the contention)
+static_assert(3 * kSlots <= QFLASH_HIP_SCALES_WORKSPACE, "workspace: 3 x kSlots partial maxima");
 
 // One tensor as `rows` runs of L contiguous elements; a run's start is
 // sum_i idx_i * in_stride_i over up to 3 outer dimensions (sizes n[], the
@@ -48,6 +52,12 @@ struct Geo {
     int nout;            // outer dimensions in use
     int64_t n[3], is[3], os[3];
     int vec;             // 16-byte chunks
+    // flat: the outer dimensions merged into one of uniform stride (rows runs,
+    // run r at r * rs in the input and r * ros in the output); the chunks of
+    // all runs are then split into equal contiguous slices, one per block
+    int flat;
+    int64_t rs, ros;
+    float inv_cpr;       // 1 / (16-byte chunks per run), for the chunk -> run split
     // element-wise fallback: the original 4-D sizes and strides
     int64_t n4[4], s4[4], o4[4];
 };
@@ -109,6 +119,22 @@ __device__ __forceinline__ int8_t quant1(float x, float s) {
     return (int8_t)(int32_t)(r < -128.0f ? -128.0f : (r > 127.0f ? 127.0f : r));
 }
 
+// fp32 quant1 through the reciprocal, for a normal scale s whose r = RN(1/s)
+// is normal: q0 = RN(x * r) = (x / s)(1 + d), |d| <= 2^-23 + 2^-48, so while
+// |x / s| < 131, q0 is within 2^-16 of x / s and within 2^-15 of RN(x / s)
+// (half an ulp, <= 2^-17, apart).  When q0 is farther than 2^-14 from every
+// half-integer, rint(q0) = rint(RN(x / s)); when |q0| >= 130, |x / s| > 129.9
+// and the clamp gives the bound either way.  The other elements (a fraction of
+// about 2^-13, and NaN) take the IEEE division.
+__device__ __forceinline__ int8_t quant1_rcp(float x, float s, float r) {
+    const float q0 = x * r;
+    if (fabsf(q0) >= 130.0f) return q0 > 0.f ? (int8_t)127 : (int8_t)-128;
+    const float n = rintf(q0);
+    const float h = 0.5f - fabsf(q0 - n);  // distance to the nearest half-integer
+    if (h > 0x1p-14f) return (int8_t)(int32_t)(n < -128.0f ? -128.0f : (n > 127.0f ? 127.0f : n));
+    return quant1<QFLASH_HIP_F32>(x, s);
+}
+
 struct GeoSet {
     Geo g[3];  // q, k, v
 };
@@ -128,16 +154,107 @@ __device__ __forceinline__ void run_start(const Geo& g, int64_t r, int64_t& in, 
     }
 }
 
+// q, k, v scales from the three absmax patterns, in T: torch divides a GPU
+// tensor by a host scalar as a product with the scalar's reciprocal in the
+// opmath type (fp32): amax * RN(1/127); scales[3] = scales[0] * scales[1].
+template <int DT>
+__device__ void write_scales(const uint32_t* m, void* scales) {
+    float s[3];
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+        s[t] = round_t<DT>(to_float<DT>(m[t]) * (1.0f / 127.0f));  // kernel.py:294-296
+        store_t<DT>(scales, t, s[t]);
+    }
+    store_t<DT>(scales, 3, round_t<DT>(s[0] * s[1]));  // (q_scale * k_scale), kernel.py:297
+}
+
 // MODE 0: absmax of the patterns into ws[tensor * kSlots + block % kSlots]
-// (atomic max; ws starts at 0).
+// (atomic max; ws is zero on entry).  Blocks are dealt to the 8 XCDs round
+// robin, so each slot is updated from one XCD only (its L2); the scales are
+// formed by a second kernel, after this one, which sees every slot.  (A
+// last-block-done counter in this kernel needs device-scope fences that write
+// back the L2 of every block's XCD: measured at twice the pass's time.)
 // MODE 1: int8 codes with scale scales[tensor].
 template <int DT, int MODE>
-__global__ __launch_bounds__(kThreads) void stream_kernel(GeoSet gs, uint32_t* ws, const void* scales) {
+__global__ __launch_bounds__(kThreads) void stream_kernel(GeoSet gs, uint32_t* ws, void* scales) {
     const Geo& g = gs.g[blockIdx.y];
-    float s = 0.f;
-    if constexpr (MODE == 1) s = load_t<DT>(scales, blockIdx.y);
+    float s = 0.f, rcp = 0.f;
+    bool rcp_ok = false;
+    if constexpr (MODE == 1) {
+        s = load_t<DT>(scales, blockIdx.y);
+        rcp = __frcp_rn(s);
+        rcp_ok = s >= 0x1p-126f && s < 0x1p126f;  // s and 1/s normal
+    }
     uint32_t m = 0;
-    if (g.vec) {
+    if (g.flat) {
+        constexpr int EPC = 16 / esize<DT>();
+        constexpr int U = 4;  // chunks in flight per thread
+        const uint32_t cpr = (uint32_t)(g.L / EPC);
+        const uint32_t F = (uint32_t)g.rows * cpr;
+        const uint32_t per = (F + gridDim.x - 1) / gridDim.x;
+        const uint32_t s0 = blockIdx.x * per, s1 = min(F, s0 + per);
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(g.p);
+        for (uint32_t base = s0 + threadIdx.x; base < s1; base += kThreads * U) {
+            u32x4 v[U];
+            int64_t out[U];
+#pragma unroll
+            for (int k = 0; k < U; ++k) {
+                const uint32_t f = base + k * kThreads;
+                if (f < s1) {
+                    // run r = f / cpr from a float estimate, corrected to the exact quotient
+                    uint32_t r = 0, c = f;
+                    if (g.rows > 1) {
+                        r = (uint32_t)((float)f * g.inv_cpr);
+                        if (r * cpr > f) --r;
+                        else if ((r + 1) * cpr <= f) ++r;
+                        c = f - r * cpr;
+                    }
+                    v[k] = __builtin_nontemporal_load(
+                        reinterpret_cast<const u32x4*>(src + ((int64_t)r * g.rs * esize<DT>() + (int64_t)c * 16)));
+                    out[k] = (int64_t)r * g.ros + (int64_t)c * EPC;
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < U; ++k) {
+                if (base + k * kThreads >= s1) break;
+                const uint32_t w[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+                if constexpr (MODE == 0) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if constexpr (DT == QFLASH_HIP_F32) {
+                            m = max(m, abs_bits<DT>(w[e]));
+                        } else {
+                            m = max(m, abs_bits<DT>(w[e] & 0xffffu));
+                            m = max(m, abs_bits<DT>(w[e] >> 16));
+                        }
+                    }
+                } else {
+                    int8_t* dst = g.o + out[k];
+                    if constexpr (DT == QFLASH_HIP_F32) {
+                        uint32_t packed = 0;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float xe = __uint_as_float(w[e]);
+                            const int8_t c = rcp_ok ? quant1_rcp(xe, s, rcp) : quant1<DT>(xe, s);
+                            packed |= (uint32_t)(uint8_t)c << (8 * e);
+                        }
+                        __builtin_nontemporal_store(packed, reinterpret_cast<uint32_t*>(dst));
+                    } else {
+                        uint32_t lo = 0, hi = 0;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const uint32_t a = (uint8_t)quant1<DT>(to_float<DT>(w[e] & 0xffffu), s);
+                            const uint32_t b = (uint8_t)quant1<DT>(to_float<DT>(w[e] >> 16), s);
+                            const uint32_t pair = a | (b << 8);
+                            if (e < 2) lo |= pair << (16 * e);
+                            else hi |= pair << (16 * (e - 2));
+                        }
+                        __builtin_nontemporal_store(u32x2{lo, hi}, reinterpret_cast<u32x2*>(dst));
+                    }
+                }
+            }
+        }
+    } else if (g.vec) {
         constexpr int EPC = 16 / esize<DT>();  // elements per 16-byte chunk
         const int64_t cpr = g.L / EPC;
         const int64_t segs = (cpr + kSeg - 1) / kSeg;
@@ -210,22 +327,17 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(GeoSet gs, uint32_t* w
     }
 }
 
-// scales[0..2] = amax / 127 (q, k, v), scales[3] = scales[0] * scales[1], all in T.
-// torch divides a GPU tensor by a host scalar as a product with the scalar's
-// reciprocal in the opmath type (fp32): amax * RN(1/127).
+// The scales from the slots of the absmax pass (one wave: lane i reads slot i
+// of each tensor), which it sets back to zero for the next call.
 template <int DT>
-__global__ __launch_bounds__(64) void scales_kernel(const uint32_t* ws, void* scales) {
+__global__ __launch_bounds__(64) void scales_kernel(uint32_t* ws, void* scales) {
     uint32_t m[3];
 #pragma unroll
-    for (int t = 0; t < 3; ++t) m[t] = wave_max(ws[t * kSlots + threadIdx.x]);
-    if (threadIdx.x != 0) return;
-    float s[3];
-#pragma unroll
     for (int t = 0; t < 3; ++t) {
-        s[t] = round_t<DT>(to_float<DT>(m[t]) * (1.0f / 127.0f));  // kernel.py:294-296
-        store_t<DT>(scales, t, s[t]);
+        m[t] = wave_max(ws[t * kSlots + threadIdx.x]);
+        ws[t * kSlots + threadIdx.x] = 0;
     }
-    store_t<DT>(scales, 3, round_t<DT>(s[0] * s[1]));  // (q_scale * k_scale), kernel.py:297
+    if (threadIdx.x == 0) write_scales<DT>(m, scales);
 }
 
 // Runs of a tensor in its memory order (see the file comment).  `o` / `os4`
@@ -281,22 +393,51 @@ static int make_geo(Geo& g, const void* p, const int64_t* n4, const int64_t* s4,
         g.vec = (g.L % epc == 0) && ((uintptr_t)p % 16 == 0) && (!o || (uintptr_t)o % epc == 0);
         for (int i = 0; i < g.nout && g.vec; ++i) g.vec = (g.is[i] % epc == 0) && (!o || g.os[i] % epc == 0);
     }
+    // flat: outer dimensions that step uniformly (stride of i = stride of i+1 times
+    // size of i+1, in the input and the output) are one dimension of runs
+    g.flat = 0;
+    if (g.vec) {
+        bool uniform = true;
+        for (int i = 0; i + 1 < g.nout && uniform; ++i)
+            uniform = g.is[i] == g.is[i + 1] * g.n[i + 1] && (!o || g.os[i] == g.os[i + 1] * g.n[i + 1]);
+        const int64_t cpr = g.L / epc;
+        if (uniform && g.rows * cpr < (1ll << 31) && g.rows < (1ll << 22)) {
+            g.flat = 1;
+            g.rs = g.nout ? g.is[g.nout - 1] : 0;
+            g.ros = g.nout ? g.os[g.nout - 1] : 0;
+            g.inv_cpr = 1.0f / (float)cpr;
+        }
+    }
     return 0;
 }
 
-static unsigned grid_x(const Geo* g, int es) {
+// Blocks per tensor.  flat: `cpt` 16-byte chunks per thread (measured on MI355X
+// at 113 MB per tensor: the absmax pass, which ends each block with an atomic,
+// is fastest at QF_ABSMAX_CPT, the quantisation pass at QF_QUANT_CPT).
+#ifndef QF_ABSMAX_CPT
+#define QF_ABSMAX_CPT 64
+#endif
+#ifndef QF_QUANT_CPT
+#define QF_QUANT_CPT 4
+#endif
+#ifndef QF_MAX_BLOCKS
+#define QF_MAX_BLOCKS 16384
+#endif
+static unsigned grid_x(const Geo* g, int es, int cpt) {
     int64_t units = 1;
     for (int i = 0; i < 3; ++i) {
-        const int64_t u = g[i].vec ? g[i].rows * ((g[i].L * es / 16 + kSeg - 1) / kSeg)
+        const int64_t u = g[i].flat ? (g[i].rows * (g[i].L * es / 16) + cpt * kThreads - 1) / (cpt * kThreads)
+                        : g[i].vec ? g[i].rows * ((g[i].L * es / 16 + kSeg - 1) / kSeg)
                                    : (g[i].n4[0] * g[i].n4[1] * g[i].n4[2] * g[i].n4[3] + kThreads - 1) / kThreads;
         units = units > u ? units : u;
     }
-    return (unsigned)(units < 2048 ? units : 2048);
+    const int64_t cap = g[0].flat && g[1].flat && g[2].flat ? QF_MAX_BLOCKS : 2048;
+    return (unsigned)(units < cap ? units : cap);
 }
 
 template <int DT>
 static int scales_dt(Geo* g, void* scales, uint32_t* ws, hipStream_t st) {
-    const dim3 grid(grid_x(g, esize<DT>()), 3);
+    const dim3 grid(grid_x(g, esize<DT>(), QF_ABSMAX_CPT), 3);
     const GeoSet gs = {{g[0], g[1], g[2]}};
     hipLaunchKernelGGL((stream_kernel<DT, 0>), grid, dim3(kThreads), 0, st, gs, ws, nullptr);
     hipLaunchKernelGGL((scales_kernel<DT>), dim3(1), dim3(64), 0, st, ws, scales);
@@ -306,9 +447,9 @@ static int scales_dt(Geo* g, void* scales, uint32_t* ws, hipStream_t st) {
 
 template <int DT>
 static int quant_dt(Geo* g, const void* scales, hipStream_t st) {
-    const dim3 grid(grid_x(g, esize<DT>()), 3);
+    const dim3 grid(grid_x(g, esize<DT>(), QF_QUANT_CPT), 3);
     const GeoSet gs = {{g[0], g[1], g[2]}};
-    hipLaunchKernelGGL((stream_kernel<DT, 1>), grid, dim3(kThreads), 0, st, gs, nullptr, scales);
+    hipLaunchKernelGGL((stream_kernel<DT, 1>), grid, dim3(kThreads), 0, st, gs, nullptr, const_cast<void*>(scales));
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : fail(QFLASH_HIP_ELAUNCH, "launch failed: %s", hipGetErrorString(e));
 }
@@ -328,9 +469,9 @@ int qflash_hip_scales(const void* q, const void* k, const void* v, int32_t dtype
         return qfq::fail(QFLASH_HIP_EINVAL, "null pointer argument");
     const int es = qfq::esize_of(dtype);
     if (!es) return qfq::fail(QFLASH_HIP_EINVAL, "unknown dtype code %d", dtype);
-    if (workspace_elems < 3 * qfq::kSlots)
+    if (workspace_elems < QFLASH_HIP_SCALES_WORKSPACE)
         return qfq::fail(QFLASH_HIP_EINVAL, "workspace holds %lld entries, %d needed", (long long)workspace_elems,
-                         3 * qfq::kSlots);
+                         QFLASH_HIP_SCALES_WORKSPACE);
     qfq::Geo g[3];
     const void* x[3] = {q, k, v};
     for (int i = 0; i < 3; ++i)

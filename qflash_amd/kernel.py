@@ -21,6 +21,7 @@ from __future__ import annotations
 import ctypes
 import os
 import statistics
+import threading
 
 import torch
 from torch import Tensor
@@ -215,6 +216,44 @@ def bench_latency_ms(fn, warmup: float = 10, rep: float = 100, flush_mb: int = 5
 _DT_CODE = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}
 
 
+_ws_cache = threading.local()
+_host_cache = threading.local()
+
+
+def _scalar_to_host(x: Tensor):
+    """Start copying the 1-element device tensor ``x`` to pinned host memory on the
+    current stream; the returned function waits for that copy only (not for work
+    queued after it) and returns ``x.item()``."""
+    bufs = getattr(_host_cache, "d", None)
+    if bufs is None:
+        bufs = _host_cache.d = {}
+    buf = bufs.get(x.dtype)
+    if buf is None:
+        buf = bufs[x.dtype] = torch.empty(1, dtype=x.dtype, pin_memory=True)
+    buf.copy_(x.reshape(1), non_blocking=True)
+    done = torch.cuda.Event()
+    done.record(torch.cuda.current_stream(x.device))
+
+    def wait():
+        done.synchronize()
+        return buf.item()
+    return wait
+
+
+def _scales_workspace(device) -> Tensor:
+    """The absmax pass's workspace for this thread and device: zeroed once, and
+    left zeroed by every call when it completes (calls of one thread follow
+    each other in stream order on one device's current stream)."""
+    cache = getattr(_ws_cache, "d", None)
+    if cache is None:
+        cache = _ws_cache.d = {}
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    ws = cache.get(key)
+    if ws is None:
+        ws = cache[key] = torch.zeros(_lib.SCALES_WORKSPACE, dtype=torch.int32, device=device)
+    return ws
+
+
 def quantize_qkv(query: Tensor, key: Tensor, value: Tensor):
     """Per-tensor scales and int8 codes of Q, K, V on the device (kernel.py:294-311).
 
@@ -245,7 +284,7 @@ def quantize_qkv(query: Tensor, key: Tensor, value: Tensor):
     code = _DT_CODE[T]
     geo = (ctypes.c_int64 * 24)(*query.shape, *query.stride(), *key.shape, *key.stride(), *value.shape,
                                  *value.stride())
-    ws = torch.zeros(_lib.SCALES_WORKSPACE, dtype=torch.int32, device=query.device)  # atomic max from 0
+    ws = _scales_workspace(query.device)
     scales = torch.empty(4, dtype=T, device=query.device)
     stream = _stream_ptr(query)
     ptrs = [ctypes.c_void_p(x.data_ptr()) for x in (query, key, value)]
@@ -324,10 +363,13 @@ def qflash_forward(
 
     scales, finish = quantize_qkv(query, key, value)  # kernel.py:294-296 on the device
     o_scale = scales[2]
-    sm_scale = scale * scales[3].item()  # the one host sync, kernel.py:297
+    qk_scale = _scalar_to_host(scales[3])
+    # kernel.py:309-311: the quantisation needs only the device scales, so it is
+    # queued before the host waits for q_scale * k_scale (the reference's one
+    # sync, kernel.py:297); the host then forms the constants while it runs
+    q8, k8, v8 = finish()
+    sm_scale = scale * qk_scale()
     sm_rscale, exp_M, req_M, l_M, acc_M = fixed_point_constants(sm_scale)
-
-    q8, k8, v8 = finish()  # kernel.py:309-311
     Z, H, N = q8.shape[0], q8.shape[1], q8.shape[2]
     consts = (sm_rscale, exp_M, req_M, l_M, acc_M)
     flag_kw = dict(EXP_USE_SHIFT=EXP_USE_SHIFT, L_USE_SHIFT=L_USE_SHIFT, ACC_USE_SHIFT=ACC_USE_SHIFT,
@@ -365,9 +407,10 @@ def qflash_forward_window(query: Tensor, key: Tensor, value: Tensor, rel_bias: T
     scale = scale * LOG2E
     scales, finish = quantize_qkv(query, key, value)
     o_scale = scales[2]
-    sm_scale = scale * scales[3].item()
-    consts = fixed_point_constants(sm_scale)
+    qk_scale = _scalar_to_host(scales[3])
     q8, k8, v8 = finish()
+    sm_scale = scale * qk_scale()
+    consts = fixed_point_constants(sm_scale)
     o = torch.empty_like(v8)
     Z, H, N = q8.shape[0], q8.shape[1], q8.shape[2]
     flag_kw = dict(EXP_USE_SHIFT=EXP_USE_SHIFT, L_USE_SHIFT=L_USE_SHIFT, ACC_USE_SHIFT=ACC_USE_SHIFT,

@@ -139,12 +139,12 @@ def test_quantiser_entries_check_arguments(lib):
     geo = (ctypes.c_int64 * 24)(*([1, 1, 4, 32, 128, 128, 32, 1] * 3))
     fake = ctypes.c_void_p(64)
     ws = ctypes.c_void_p(64)
-    assert lib.qflash_hip_scales(fake, fake, fake, 9, geo, fake, ws, 192, None) == -1
+    assert lib.qflash_hip_scales(fake, fake, fake, 9, geo, fake, ws, _lib.SCALES_WORKSPACE, None) == -1
     assert b"dtype" in lib.qflash_hip_last_error()
     assert lib.qflash_hip_scales(fake, fake, fake, _lib.F32, geo, fake, ws, 3, None) == -1
     assert b"workspace" in lib.qflash_hip_last_error()
     bad = (ctypes.c_int64 * 24)(*([1, 1, 0, 32, 128, 128, 32, 1] * 3))
-    assert lib.qflash_hip_scales(fake, fake, fake, _lib.F32, bad, fake, ws, 192, None) == -1
+    assert lib.qflash_hip_scales(fake, fake, fake, _lib.F32, bad, fake, ws, _lib.SCALES_WORKSPACE, None) == -1
     assert b"empty" in lib.qflash_hip_last_error()
     ost = (ctypes.c_int64 * 12)(*([128, 128, 32, 1] * 3))
     assert lib.qflash_hip_quantize(fake, fake, fake, _lib.F32, geo, None, fake, fake, ost, fake, None) == -1

@@ -107,3 +107,33 @@ def test_fused_dequantisation_equals_codes_times_scale(dtype, masked):
         want = o8 * scales[2]
         assert want.dtype == dtype and want.stride() == out.stride()
         assert torch.equal(out, want), (dtype, masked, general)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_codes_near_half_integers_match_torch(seed):
+    """fp32 quantisation goes through the reciprocal of the scale except near
+    half-integer quotients: values on, just above and just below (k + 1/2)*s
+    for every k, and their float neighbours, must round as torch's division."""
+    from qflash_amd.kernel import quantize_qkv
+    g = torch.Generator().manual_seed(seed)
+    amax = float(torch.empty(1).uniform_(0.5, 40.0, generator=g))
+    s = torch.tensor(amax) / 127  # the scale the device computes from amax
+    ks = torch.arange(-129, 129, dtype=torch.float32) + 0.5
+    base = (ks * s).to(torch.float32)
+    up = torch.nextafter(base, torch.tensor(float("inf")))
+    dn = torch.nextafter(base, torch.tensor(float("-inf")))
+    vals = torch.cat([base, up, dn, torch.nextafter(up, torch.tensor(float("inf"))),
+                      torch.nextafter(dn, torch.tensor(float("-inf")))])
+    vals = vals.clamp(-amax, amax)
+    n = 32 * 64
+    q = torch.empty(n).uniform_(-amax, amax, generator=g)
+    q[: vals.numel()] = vals
+    q[-1] = amax  # fixes the absmax
+    q = q.view(1, 1, 32, 64).to(DEV)
+    k = (torch.randn(1, 1, 32, 64, generator=g) * 5).to(DEV)
+    want_scales, want_codes = _torch_ref(q, k, q)
+    scales, finish = quantize_qkv(q, k, q)
+    codes = finish()
+    assert torch.equal(scales, want_scales)
+    for c, w in zip(codes, want_codes):
+        assert torch.equal(c, w)
