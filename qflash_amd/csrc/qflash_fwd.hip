@@ -806,20 +806,17 @@ __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& 
             if (!TAIL || !padded(v, tcut)) smin = min(smin, s[v]);
         }
     } else if (need_min) {
-        if constexpr (TAIL) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v)
-                if (!padded(v, tcut)) smin = min(smin, s[v]);
-        } else {
-            smin = min3(s[0], s[1], s[2]);
-            smin = min3(smin, s[3], s[4]);
-            smin = min3(smin, s[5], s[6]);
-            smin = min3(smin, s[7], s[8]);
-            smin = min3(smin, s[9], s[10]);
-            smin = min3(smin, s[11], s[12]);
-            smin = min3(smin, s[13], s[14]);
-            smin = min(smin, s[15]);
-        }
+        // over all 16 raw scores: a padded column's raw score (its K row reads
+        // as 0) is 0, which can only lower the minimum, so a check that passes
+        // with it passes for the real columns
+        smin = min3(s[0], s[1], s[2]);
+        smin = min3(smin, s[3], s[4]);
+        smin = min3(smin, s[5], s[6]);
+        smin = min3(smin, s[7], s[8]);
+        smin = min3(smin, s[9], s[10]);
+        smin = min3(smin, s[11], s[12]);
+        smin = min3(smin, s[13], s[14]);
+        smin = min(smin, s[15]);
     }
     if constexpr (TAIL) {
 #pragma unroll
@@ -862,7 +859,9 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     // table path: every real column of the wave has u = m' - s <= lut_lim
     // (lut_mode 1: proved for the whole row block from ||q||_1)
     bool lut_ok = false;
-    if constexpr (!TAIL) lut_ok = lut_mode == 1 || (lut_mode == 2 && __all((int64_t)mn - smin <= a.lut_lim));
+    // (mn >= smin: the difference is exact as an unsigned 32-bit value)
+    if constexpr (!TAIL || !MASKED)
+        lut_ok = lut_mode == 1 || (lut_mode == 2 && __all((uint32_t)(mn - smin) <= (uint32_t)a.lut_lim));
     bool vec_ok = wave_fast;
     if constexpr (MASKED)
         vec_ok = vec_ok && __all(smin > -(1 << 23) && mn < (1 << 23) && (int64_t)mn - smin <= xlim);
@@ -924,6 +923,14 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     lij = __builtin_amdgcn_sdot4((int)pk[2], 0x01010101, lij, false);
     lij = __builtin_amdgcn_sdot4((int)pk[3], 0x01010101, lij, false);
     lij = half_sum(lij);
+    if constexpr (TAIL && !MASKED) {
+        // Table path of the last, partial step: a padded column (score NEG_INF)
+        // read entry min(mn - NEG_INF, lut_n - 1), which is its exact p when
+        // mn - NEG_INF <= lut_lim and 0 otherwise; its P.V term is 0 either way
+        // (V rows past N read as 0), so only l needs the padded columns' p then.
+        if (lut_ok && (uint32_t)(mn - kNegInf) > (uint32_t)a.lut_lim)
+            lij = wadd(lij, (32 - (a.N - kstart)) * requant(exp2_i32(wsub(kNegInf, mn), a), a));
+    }
 
     // kernel.py:163-165
     int32_t alpha;
@@ -1121,11 +1128,11 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
         const int8_t* lk = buf + th * 32 * D;
         const int8_t* lv = buf + S::KBYTES + th * 32 * D;
         if (nfull == 0)
-            fast_step<D, MASKED, true, WIDE, DYN, true>(st, a, qv, lk, lv, fr, brow, 0, lane, wave_fast, xlim, 0,
-                                                        lut_base);
+            fast_step<D, MASKED, true, WIDE, DYN, true>(st, a, qv, lk, lv, fr, brow, 0, lane, wave_fast, xlim,
+                                                        lut_mode, lut_base);
         else
             fast_step<D, MASKED, true, WIDE, DYN, false>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane, wave_fast,
-                                                         xlim, 0, lut_base);
+                                                         xlim, lut_mode, lut_base);
     }
     if (!active) return;
     fast_store<D>(st, a, z, h, lane, q0);
