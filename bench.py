@@ -187,9 +187,15 @@ def cpu_baseline(w, threads: int):
 
 
 def run_config(name: str, steps: int, warmup: int, dev, seed: int = 0, cpu: bool = False,
-               dense_bias: bool = False):
+               dense_bias: bool = False, time_ms=None):
+    """One configuration: `steps` timed launches after `warmup` ones, or, with
+    time_ms = (warmup ms, timed ms), counts derived from a 3-launch estimate."""
     w = prepare(name, seed, dev, dense_bias=dense_bias)
     step = make_step(w)
+    if time_ms is not None:
+        _, est_ms, _ = time_steps(step, 3, 1)
+        warmup = int(min(400, max(5, time_ms[0] / est_ms)))
+        steps = int(min(1000, max(10, time_ms[1] / est_ms)))
     wall_ms, ev_mean_ms, ev_med_ms = time_steps(step, steps, warmup)
     cfg = w["cfg"]
     res = {"config": name + ("-dense-bias" if dense_bias else ""), "workload": cfg.name, "ops": cfg.ops,
@@ -324,11 +330,12 @@ def main(argv=None):
     if args.all_configs:
         per = []
         for name in CONFIGS:
-            r = head if name == args.config else run_config(name, max(5, args.steps // 5), 3, dev, args.seed)
+            # about 50 ms of warmup (the clocks settle) and 100 ms of timed launches per configuration
+            r = head if name == args.config else run_config(name, 0, 0, dev, args.seed, time_ms=(50.0, 100.0))
             per.append({k: r[k] for k in ("config", "us_per_call", "us_per_call_flushed", "kernel_tops",
                                           "sqnr_db", "hbm_gbs_algorithmic", "e2e_us")})
             if CONFIGS[name].swin:  # the reference's materialised (Z, H, N, N) bias, for comparison
-                r = run_config(name, max(5, args.steps // 5), 3, dev, args.seed, dense_bias=True)
+                r = run_config(name, 0, 0, dev, args.seed, dense_bias=True, time_ms=(50.0, 100.0))
                 per.append({k: r[k] for k in ("config", "us_per_call", "us_per_call_flushed", "kernel_tops",
                                               "sqnr_db", "hbm_gbs_algorithmic", "e2e_us")})
         line["per_config"] = per

@@ -1031,14 +1031,17 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
 // ((N-1)*so2 + D bytes from the head's base, so2 >= D checked by the host)
 // and are dropped by the hardware.
 template <int D>
-__device__ __forceinline__ void fast_store(const FastState<D>& st, const Args& a, int z, int h, int lane, int q0) {
+__device__ __forceinline__ void fast_store(const FastState<D>& st, const Args& a, int z, int h, int lane, int q0,
+                                           double* yslot) {
     constexpr int DB = D / 32;
     const int lq = lane & 31, g = lane >> 5;
     const float b_row = (float)st.l;            // S layout: lane = row
     const double y_row = 1.0 / (double)b_row;
-    const int32_t y_lo = (int32_t)(uint32_t)__double_as_longlong(y_row);
-    const int32_t y_hi = (int32_t)(uint32_t)((uint64_t)__double_as_longlong(y_row) >> 32);
     const bool exact = __any(st.l >= -1 && st.l <= 1);
+    // y of the 32 rows to LDS (this wave's 256 bytes), read back two rows at a
+    // time in the O layout (rows 8(v>>2) + 4g + (v&3), v and v+1 adjacent):
+    // 8 broadcast reads instead of 32 lane permutes
+    if (!exact && g == 0) yslot[lq] = y_row;
     const int32_t so2 = (int32_t)a.so[2];
     const __amdgpu_buffer_rsrc_t rsrc = out_rsrc(a, z, h, D);
     const float os = a.out_dt == QFLASH_HIP_I8 ? 0.f : scale_value(a);
@@ -1049,9 +1052,7 @@ __device__ __forceinline__ void fast_store(const FastState<D>& st, const Args& a
             const int row = crow(v, lane);
             const int32_t soff = (8 * (v >> 2) + (v & 3)) * so2;
             if (!exact) {
-                const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * row, y_lo);
-                const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * row, y_hi);
-                const double yd = __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+                const double yd = yslot[row];
 #pragma unroll
                 for (int t = 0; t < DB; ++t) {
                     const float qf = (float)((double)(float)st.acc[t][v] * yd);
@@ -1100,6 +1101,7 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
     dma.issue(rk, rv, smem, 0, a, wave);
     stage_sync();
 
+    static_assert(S::BYTES >= W * 256, "epilogue slots of 256 bytes per wave in one stage buffer");
     const int nfull = a.N >> 5;
     const int nstage = (a.N + S::KEYS - 1) / S::KEYS;
     // step 0 (m = NEG_INF, acc = 0) apart from the loop: the loop body then
@@ -1135,13 +1137,19 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
                                                          xlim, lut_mode, lut_base);
     }
     if (!active) return;
-    fast_store<D>(st, a, z, h, lane, q0);
+    // this wave's 256 bytes of the stage buffer that no step reads any more:
+    // the last stage used buffer (nstage - 1) & 1 and every wave has passed the
+    // barrier after the stage before it
+    fast_store<D>(st, a, z, h, lane, q0,
+                  reinterpret_cast<double*>(smem + (nstage & 1) * S::BYTES + wave * 256));
 }
 
 // Occupancy target (waves per SIMD) by head dim: the register budget of the
-// O accumulators (D/32 x 16 VGPRs) and the score / exp temporaries.
+// O accumulators (D/32 x 16 VGPRs) and the score / exp temporaries.  D = 32
+// fits 6 (80 VGPRs, no spills; measured 5 % faster than 4 on Swin windows,
+// 8 slower).
 template <int D>
-constexpr int fast_waves_per_simd() { return D <= 32 ? 4 : (D == 64 ? QF_FAST_WAVES_D64 : 2); }
+constexpr int fast_waves_per_simd() { return D <= 32 ? 6 : (D == 64 ? QF_FAST_WAVES_D64 : 2); }
 
 template <int D, int W, bool MASKED, bool DYN>
 __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Args a) {
