@@ -249,8 +249,9 @@ def e2e_us(w, dev, reps: int = 10) -> float:
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # defaults: ~40 ms of warmup (the clocks settle) and ~50 ms of timed launches at cfg3
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--config", default="cfg3")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--all-configs", action="store_true", help="also time cfg1..cfg5 (per_config field)")
