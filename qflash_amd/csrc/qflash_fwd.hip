@@ -389,7 +389,7 @@ __device__ __forceinline__ int32_t mad24(int32_t a, int32_t b, int32_t c) { retu
 __device__ __forceinline__ int32_t max3(int32_t a, int32_t b, int32_t c) { return max(max(a, b), c); }
 __device__ __forceinline__ int32_t min3(int32_t a, int32_t b, int32_t c) { return min(min(a, b), c); }
 
-// K / V stages of 64 keys (two rescale steps) per LDS buffer.  Both tiles
+// K / V stages of 32 * STEPS keys (STEPS rescale steps) per LDS buffer.  Both tiles
 // hold rows of D bytes exactly as in HBM, copied there by buffer loads that
 // write LDS directly (no registers, no VALU), with the 16-byte chunks of each
 // row permuted by an XOR swizzle so that the MFMA operand reads are free of
@@ -401,12 +401,19 @@ __device__ __forceinline__ int32_t min3(int32_t a, int32_t b, int32_t c) { retur
 //      chunk -> 16 distinct 2-bank groups.
 // Keys past N read as zeros (buffer range check), as the reference's
 // boundary-checked loads of K and V do.
-#ifndef QF_STAGE_STEPS
-#define QF_STAGE_STEPS 2
+// Steps per stage: 4 at D = 64 with 4 waves per workgroup (one barrier per 128
+// keys; 2.3 % faster than 2 at ViT-B/384, and 36 KiB of LDS per workgroup
+// keeps 4 workgroups per CU); 2 otherwise, where the LDS of more, smaller
+// workgroups (D = 32 at 6 waves per SIMD, W < 4) or of D = 128 limits it.
+#ifdef QF_STAGE_STEPS
+template <int D, int W> constexpr int stage_steps() { return QF_STAGE_STEPS; }
+#else
+template <int D, int W> constexpr int stage_steps() { return D == 64 && W == 4 ? 4 : 2; }
 #endif
-template <int D>
+template <int D, int W = 4>
 struct Stage {
-    static constexpr int STEPS = QF_STAGE_STEPS;  // 32-key rescale steps per stage
+    static constexpr int STEPS = stage_steps<D, W>();  // 32-key rescale steps per stage
+    static_assert(STEPS >= 1 && STEPS <= 4, "stages of at most 128 keys (host offset check)");
     static constexpr int KEYS = 32 * STEPS;
     static constexpr int CPR = D / 16;       // 16-byte chunks per row
     static constexpr int KBYTES = KEYS * D;  // one tile (K or V)
@@ -500,7 +507,7 @@ __device__ __forceinline__ void read_vt(i32x4* vf, const int8_t* lv, const Frag<
 // workgroup fills slots [r*NT + 64w, r*NT + 64w + 64) in round r.
 template <int D, int W>
 struct StageDma {
-    using S = Stage<D>;
+    using S = Stage<D, W>;
     static constexpr int NT = 64 * W;
     static constexpr int R = (S::SLOTS + NT - 1) / NT;
     uint32_t vk[R], vv[R];
@@ -1080,7 +1087,7 @@ template <int D, int W, bool MASKED, bool WIDE, bool DYN>
 __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t* smem, const int8_t* kb,
                                           const int8_t* vb, int z, int h, const BiasRow& brow, int wave, int lane,
                                           int q0, bool active, bool wave_fast, int32_t xlim, int lut_mode) {
-    using S = Stage<D>;
+    using S = Stage<D, W>;
     constexpr int DB = D / 32;
     const uint32_t lut_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t*)(smem + 2 * S::BYTES);
     FastState<D> st;
@@ -1153,7 +1160,7 @@ constexpr int fast_waves_per_simd() { return D <= 32 ? 6 : (D == 64 ? QF_FAST_WA
 
 template <int D, int W, bool MASKED, bool DYN>
 __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Args a) {
-    using S = Stage<D>;
+    using S = Stage<D, W>;
     constexpr int DB = D / 32;
     __shared__ __attribute__((aligned(16))) int8_t smem[2 * S::BYTES + kLutMax];
 
@@ -1387,9 +1394,10 @@ static bool choose_fast(Args& a, int D, bool masked, bool vec) {
     if (D > 128) return false;  // D=256 would spill: the general kernel serves it
     if (!vec || a.so[3] != 1) return false;
     // buffer accesses of K, V (loads) and O (stores): rows >= N must fall past
-    // (N-1)*stride + D, and the last stage's offsets (keys < N + 64) fit 31 bits
+    // (N-1)*stride + D, and the last stage's offsets (keys < N + 128, stages of
+    // at most 128 keys) fit 31 bits
     for (int64_t st : {a.sk[2], a.sv[2], a.so[2]})
-        if (st < D || (int64_t)(a.N + 64) * st + D > INT32_MAX) return false;
+        if (st < D || (int64_t)(a.N + 128) * st + D > INT32_MAX) return false;
     if (!a.exp_mode || !a.acc_mode || !a.l_mode) return false;
     if (a.acc_shift < 1 || a.acc_shift > 30 || a.l_shift < 1 || a.l_shift > 30) return false;
     if ((int64_t)a.rs * a.aM >= (1ll << 31) || (int64_t)a.rs * a.lM >= (1ll << 31)) return false;
