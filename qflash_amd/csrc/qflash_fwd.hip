@@ -45,6 +45,13 @@ constexpr int32_t kNegInf = -(1 << 20);  // kernel.py:137
 #endif
 constexpr int kBN = 32;                   // kernel.py:27, one rescale step
 constexpr int kLutMax = 4096;             // bytes of LDS for the p(u) table of the fast kernel
+// The unmasked fast kernel carries every score (and the running max) plus
+// kScoreBias: one extra MFMA of two all-(-128) operands starts each score tile
+// at 32 * 128 * 128.  Every difference the algorithm takes is unchanged, and a
+// wave whose scores stay above -kScoreBias + kLutMax (128 * ||q_row||_1 below
+// that) has all scores and table thresholds positive, so one saturating
+// subtraction per score gives its table index.
+constexpr int32_t kScoreBias = 32 * 128 * 128;
 
 struct Args {
     const int8_t* q;
@@ -600,155 +607,107 @@ __device__ __forceinline__ int32_t exp2_fast(int32_t x, int32_t eM, int32_t rs) 
 // E = ((r >> 1) + rs) >> q is 0 once 2^q exceeds rs + max(0, r/2) (true for
 // q >= bitlen(rs) + 3 when kappa <= 2|eM|) as long as r >= -2rs (all u when
 // kappa >= 0, u <= rs*2^16/|kappa| otherwise); p(E = 0) = 0.  The table holds
-// p(u) for u = 0 .. lut_n - 1 (its last entry 0), every u up to lut_lim reads
-// entry min(u, lut_n - 1), and a step uses the table only when all of its
-// real columns have u <= lut_lim.  Clamping also makes the many far-off
-// columns of a step read one byte (a broadcast, no LDS bank conflict): with
-// the addresses left spread over a table of 8 KB the kernel is slower
-// (measured).  The table lives in LDS after the K / V
-// stages; `addr` are LDS byte addresses.  Each byte load fills bits 0-7 of
-// its own register (the half-register d16 loads are no use here: with
-// SRAM ECC on, as on MI355X, they clear the other half), and three
+// p(u) for u = 0 .. lut_n - 1 (its last entry 0) in reverse order, entry
+// j = lut_n - 1 - u, so that the index of every u up to lut_lim is
+// max(s - thr, 0) with thr = m' - (lut_n - 1): one saturating subtraction per
+// score when scores and thr are positive (kScoreBias), a subtraction and a
+// max otherwise.  A step uses the table only when all of its real columns
+// have u <= lut_lim.  Clamping also makes the many far-off columns of a step
+// read one byte (a broadcast, no LDS bank conflict): with the addresses left
+// spread over a table of 8 KB the kernel is slower (measured).  The table
+// lives in LDS after the K / V stages, at the compile-time LDS address LUT
+// (the kernel's only LDS array starts at address 0; the kernel checks it),
+// which the byte loads take as their immediate offset.  Each byte load fills
+// bits 0-7 of its own register (the half-register d16 loads are no use here:
+// with SRAM ECC on, as on MI355X, they clear the other half), and three
 // shift-ors pack four p values into the MFMA A operand's byte order.  The
 // step's V^T fragment reads (read_vt) go out in the same asm block, so one
 // LDS wait covers both; the compiler's own packing of byte loads would take
 // 4.5 instructions per four bytes, and it would wait for the in-flight
 // stage copy before every LDS read.
-template <int D>
-__device__ __forceinline__ void lut_pack_vt(uint32_t* pk, i32x4* vf, const uint32_t* addr, const int8_t* lv,
+#define QF_LUT_LOADS                                   \
+    "ds_read_u8 %0, %0 offset:%c[lut]\n\t"             \
+    "ds_read_u8 %1, %1 offset:%c[lut]\n\t"             \
+    "ds_read_u8 %2, %2 offset:%c[lut]\n\t"             \
+    "ds_read_u8 %3, %3 offset:%c[lut]\n\t"             \
+    "ds_read_u8 %4, %4 offset:%c[lut]\n\t"             \
+    "ds_read_u8 %5, %5 offset:%c[lut]\n\t"             \
+    "ds_read_u8 %6, %6 offset:%c[lut]\n\t"             \
+    "ds_read_u8 %7, %7 offset:%c[lut]\n\t"             \
+    "ds_read_u8 %8, %8 offset:%c[lut]\n\t"             \
+    "ds_read_u8 %9, %9 offset:%c[lut]\n\t"             \
+    "ds_read_u8 %10, %10 offset:%c[lut]\n\t"           \
+    "ds_read_u8 %11, %11 offset:%c[lut]\n\t"           \
+    "ds_read_u8 %12, %12 offset:%c[lut]\n\t"           \
+    "ds_read_u8 %13, %13 offset:%c[lut]\n\t"           \
+    "ds_read_u8 %14, %14 offset:%c[lut]\n\t"           \
+    "ds_read_u8 %15, %15 offset:%c[lut]\n\t"
+#define QF_LUT_PACK                                    \
+    "s_waitcnt lgkmcnt(0)\n\t"                          \
+    "v_lshl_or_b32 %0, %1, 8, %0\n\t"                   \
+    "v_lshl_or_b32 %2, %3, 8, %2\n\t"                   \
+    "v_lshl_or_b32 %0, %2, 16, %0\n\t"                  \
+    "v_lshl_or_b32 %4, %5, 8, %4\n\t"                   \
+    "v_lshl_or_b32 %6, %7, 8, %6\n\t"                   \
+    "v_lshl_or_b32 %4, %6, 16, %4\n\t"                  \
+    "v_lshl_or_b32 %8, %9, 8, %8\n\t"                   \
+    "v_lshl_or_b32 %10, %11, 8, %10\n\t"                \
+    "v_lshl_or_b32 %8, %10, 16, %8\n\t"                 \
+    "v_lshl_or_b32 %12, %13, 8, %12\n\t"                \
+    "v_lshl_or_b32 %14, %15, 8, %14\n\t"                \
+    "v_lshl_or_b32 %12, %14, 16, %12"
+#define QF_LUT_IDX_OPERANDS                                                                                  \
+    "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),         \
+        "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]), "+v"(r[12]), "+v"(r[13]), "+v"(r[14]), "+v"(r[15])
+
+template <int D, int LUT>
+__device__ __forceinline__ void lut_pack_vt(uint32_t* pk, i32x4* vf, const uint32_t* idx, const int8_t* lv,
                                             const Frag<D>& fr) {
+    static_assert(LUT >= 0 && LUT + kLutMax <= 65536, "table offset must fit the 16-bit LDS immediate");
     typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
     const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)lv;
-    // each byte load writes its result over its own address register
+    // each byte load writes its result over its own index register
     uint32_t r[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) r[i] = addr[i];
+    for (int i = 0; i < 16; ++i) r[i] = idx[i];
     i32x2 t[2 * (D / 32)];
     if constexpr (D == 32) {
-        asm volatile(
-            "ds_read_u8 %0, %0\n\t"
-            "ds_read_u8 %1, %1\n\t"
-            "ds_read_u8 %2, %2\n\t"
-            "ds_read_u8 %3, %3\n\t"
-            "ds_read_u8 %4, %4\n\t"
-            "ds_read_u8 %5, %5\n\t"
-            "ds_read_u8 %6, %6\n\t"
-            "ds_read_u8 %7, %7\n\t"
-            "ds_read_u8 %8, %8\n\t"
-            "ds_read_u8 %9, %9\n\t"
-            "ds_read_u8 %10, %10\n\t"
-            "ds_read_u8 %11, %11\n\t"
-            "ds_read_u8 %12, %12\n\t"
-            "ds_read_u8 %13, %13\n\t"
-            "ds_read_u8 %14, %14\n\t"
-            "ds_read_u8 %15, %15\n\t"
-            "ds_read_b64_tr_b8 %16, %18\n\t"
-            "ds_read_b64_tr_b8 %17, %18 offset:%c19\n\t"
-            "s_waitcnt lgkmcnt(0)\n\t"
-            "v_lshl_or_b32 %0, %1, 8, %0\n\t"
-            "v_lshl_or_b32 %2, %3, 8, %2\n\t"
-            "v_lshl_or_b32 %0, %2, 16, %0\n\t"
-            "v_lshl_or_b32 %4, %5, 8, %4\n\t"
-            "v_lshl_or_b32 %6, %7, 8, %6\n\t"
-            "v_lshl_or_b32 %4, %6, 16, %4\n\t"
-            "v_lshl_or_b32 %8, %9, 8, %8\n\t"
-            "v_lshl_or_b32 %10, %11, 8, %10\n\t"
-            "v_lshl_or_b32 %8, %10, 16, %8\n\t"
-            "v_lshl_or_b32 %12, %13, 8, %12\n\t"
-            "v_lshl_or_b32 %14, %15, 8, %14\n\t"
-            "v_lshl_or_b32 %12, %14, 16, %12"
-            : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),
-              "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]), "+v"(r[12]), "+v"(r[13]), "+v"(r[14]), "+v"(r[15]),
-              "=&v"(t[0]), "=&v"(t[1])
-            : "v"(base + fr.v[0]), "i"(16 * D));
+        asm volatile(QF_LUT_LOADS
+                     "ds_read_b64_tr_b8 %[t0], %[b0]\n\t"
+                     "ds_read_b64_tr_b8 %[t1], %[b0] offset:%c[vo]\n\t" QF_LUT_PACK
+                     : QF_LUT_IDX_OPERANDS, [t0] "=&v"(t[0]), [t1] "=&v"(t[1])
+                     : [b0] "v"(base + fr.v[0]), [vo] "i"(16 * D), [lut] "i"(LUT));
     } else if constexpr (D == 64) {
-        asm volatile(
-            "ds_read_u8 %0, %0\n\t"
-            "ds_read_u8 %1, %1\n\t"
-            "ds_read_u8 %2, %2\n\t"
-            "ds_read_u8 %3, %3\n\t"
-            "ds_read_u8 %4, %4\n\t"
-            "ds_read_u8 %5, %5\n\t"
-            "ds_read_u8 %6, %6\n\t"
-            "ds_read_u8 %7, %7\n\t"
-            "ds_read_u8 %8, %8\n\t"
-            "ds_read_u8 %9, %9\n\t"
-            "ds_read_u8 %10, %10\n\t"
-            "ds_read_u8 %11, %11\n\t"
-            "ds_read_u8 %12, %12\n\t"
-            "ds_read_u8 %13, %13\n\t"
-            "ds_read_u8 %14, %14\n\t"
-            "ds_read_u8 %15, %15\n\t"
-            "ds_read_b64_tr_b8 %16, %20\n\t"
-            "ds_read_b64_tr_b8 %17, %20 offset:%c22\n\t"
-            "ds_read_b64_tr_b8 %18, %21\n\t"
-            "ds_read_b64_tr_b8 %19, %21 offset:%c22\n\t"
-            "s_waitcnt lgkmcnt(0)\n\t"
-            "v_lshl_or_b32 %0, %1, 8, %0\n\t"
-            "v_lshl_or_b32 %2, %3, 8, %2\n\t"
-            "v_lshl_or_b32 %0, %2, 16, %0\n\t"
-            "v_lshl_or_b32 %4, %5, 8, %4\n\t"
-            "v_lshl_or_b32 %6, %7, 8, %6\n\t"
-            "v_lshl_or_b32 %4, %6, 16, %4\n\t"
-            "v_lshl_or_b32 %8, %9, 8, %8\n\t"
-            "v_lshl_or_b32 %10, %11, 8, %10\n\t"
-            "v_lshl_or_b32 %8, %10, 16, %8\n\t"
-            "v_lshl_or_b32 %12, %13, 8, %12\n\t"
-            "v_lshl_or_b32 %14, %15, 8, %14\n\t"
-            "v_lshl_or_b32 %12, %14, 16, %12"
-            : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),
-              "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]), "+v"(r[12]), "+v"(r[13]), "+v"(r[14]), "+v"(r[15]),
-              "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3])
-            : "v"(base + fr.v[0]), "v"(base + fr.v[1]), "i"(16 * D));
+        asm volatile(QF_LUT_LOADS
+                     "ds_read_b64_tr_b8 %[t0], %[b0]\n\t"
+                     "ds_read_b64_tr_b8 %[t1], %[b0] offset:%c[vo]\n\t"
+                     "ds_read_b64_tr_b8 %[t2], %[b1]\n\t"
+                     "ds_read_b64_tr_b8 %[t3], %[b1] offset:%c[vo]\n\t" QF_LUT_PACK
+                     : QF_LUT_IDX_OPERANDS, [t0] "=&v"(t[0]), [t1] "=&v"(t[1]), [t2] "=&v"(t[2]), [t3] "=&v"(t[3])
+                     : [b0] "v"(base + fr.v[0]), [b1] "v"(base + fr.v[1]), [vo] "i"(16 * D), [lut] "i"(LUT));
     } else {
-        asm volatile(
-            "ds_read_u8 %0, %0\n\t"
-            "ds_read_u8 %1, %1\n\t"
-            "ds_read_u8 %2, %2\n\t"
-            "ds_read_u8 %3, %3\n\t"
-            "ds_read_u8 %4, %4\n\t"
-            "ds_read_u8 %5, %5\n\t"
-            "ds_read_u8 %6, %6\n\t"
-            "ds_read_u8 %7, %7\n\t"
-            "ds_read_u8 %8, %8\n\t"
-            "ds_read_u8 %9, %9\n\t"
-            "ds_read_u8 %10, %10\n\t"
-            "ds_read_u8 %11, %11\n\t"
-            "ds_read_u8 %12, %12\n\t"
-            "ds_read_u8 %13, %13\n\t"
-            "ds_read_u8 %14, %14\n\t"
-            "ds_read_u8 %15, %15\n\t"
-            "ds_read_b64_tr_b8 %16, %24\n\t"
-            "ds_read_b64_tr_b8 %17, %24 offset:%c28\n\t"
-            "ds_read_b64_tr_b8 %18, %25\n\t"
-            "ds_read_b64_tr_b8 %19, %25 offset:%c28\n\t"
-            "ds_read_b64_tr_b8 %20, %26\n\t"
-            "ds_read_b64_tr_b8 %21, %26 offset:%c28\n\t"
-            "ds_read_b64_tr_b8 %22, %27\n\t"
-            "ds_read_b64_tr_b8 %23, %27 offset:%c28\n\t"
-            "s_waitcnt lgkmcnt(0)\n\t"
-            "v_lshl_or_b32 %0, %1, 8, %0\n\t"
-            "v_lshl_or_b32 %2, %3, 8, %2\n\t"
-            "v_lshl_or_b32 %0, %2, 16, %0\n\t"
-            "v_lshl_or_b32 %4, %5, 8, %4\n\t"
-            "v_lshl_or_b32 %6, %7, 8, %6\n\t"
-            "v_lshl_or_b32 %4, %6, 16, %4\n\t"
-            "v_lshl_or_b32 %8, %9, 8, %8\n\t"
-            "v_lshl_or_b32 %10, %11, 8, %10\n\t"
-            "v_lshl_or_b32 %8, %10, 16, %8\n\t"
-            "v_lshl_or_b32 %12, %13, 8, %12\n\t"
-            "v_lshl_or_b32 %14, %15, 8, %14\n\t"
-            "v_lshl_or_b32 %12, %14, 16, %12"
-            : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),
-              "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]), "+v"(r[12]), "+v"(r[13]), "+v"(r[14]), "+v"(r[15]),
-              "=&v"(t[0]), "=&v"(t[1]), "=&v"(t[2]), "=&v"(t[3]), "=&v"(t[4]), "=&v"(t[5]), "=&v"(t[6]), "=&v"(t[7])
-            : "v"(base + fr.v[0]), "v"(base + fr.v[1]), "v"(base + fr.v[2]), "v"(base + fr.v[3]), "i"(16 * D));
+        asm volatile(QF_LUT_LOADS
+                     "ds_read_b64_tr_b8 %[t0], %[b0]\n\t"
+                     "ds_read_b64_tr_b8 %[t1], %[b0] offset:%c[vo]\n\t"
+                     "ds_read_b64_tr_b8 %[t2], %[b1]\n\t"
+                     "ds_read_b64_tr_b8 %[t3], %[b1] offset:%c[vo]\n\t"
+                     "ds_read_b64_tr_b8 %[t4], %[b2]\n\t"
+                     "ds_read_b64_tr_b8 %[t5], %[b2] offset:%c[vo]\n\t"
+                     "ds_read_b64_tr_b8 %[t6], %[b3]\n\t"
+                     "ds_read_b64_tr_b8 %[t7], %[b3] offset:%c[vo]\n\t" QF_LUT_PACK
+                     : QF_LUT_IDX_OPERANDS, [t0] "=&v"(t[0]), [t1] "=&v"(t[1]), [t2] "=&v"(t[2]), [t3] "=&v"(t[3]),
+                       [t4] "=&v"(t[4]), [t5] "=&v"(t[5]), [t6] "=&v"(t[6]), [t7] "=&v"(t[7])
+                     : [b0] "v"(base + fr.v[0]), [b1] "v"(base + fr.v[1]), [b2] "v"(base + fr.v[2]),
+                       [b3] "v"(base + fr.v[3]), [vo] "i"(16 * D), [lut] "i"(LUT));
     }
 #pragma unroll
     for (int w = 0; w < 4; ++w) pk[w] = r[4 * w];
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) vf[i] = i32x4{t[2 * i].x, t[2 * i].y, t[2 * i + 1].x, t[2 * i + 1].y};
 }
+#undef QF_LUT_LOADS
+#undef QF_LUT_PACK
+#undef QF_LUT_IDX_OPERANDS
 
 // Per-wave state of the fast kernel (S layout for m, l, bnd: lane = query;
 // O layout for acc).
@@ -793,10 +752,12 @@ __device__ __forceinline__ void load_bias(int32_t* bias_v, const Args& a, const 
 // S^T tile of one step with bias and padding applied (kernel.py:153-156, :250-253);
 // returns the row max over the 32 columns (both lane halves).
 // smin: the minimum over the real columns when MASKED or need_min (else INT32_MAX).
+// Unmasked: every score carries kScoreBias, from an extra MFMA of xb (all
+// bytes -128) with itself.
 template <int D, bool MASKED, bool TAIL>
 __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& a, const i32x4* qv,
                                           const int8_t* lk, const Frag<D>& fr, const int32_t* bias_v, int kstart,
-                                          int lane, bool need_min) {
+                                          int lane, bool need_min, i32x4 xb) {
     constexpr int DB = D / 32;
     s = i32x16{};
 #pragma unroll
@@ -804,6 +765,7 @@ __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& 
         const i32x4 kf = *reinterpret_cast<const i32x4*>(lk + fr.k[db]);
         s = mfma32(kf, qv[db], s);
     }
+    if constexpr (!MASKED) s = mfma32(xb, xb, s);
     smin = INT32_MAX;
     const int32_t tcut = a.N - kstart - 4 * (lane >> 5);
     if constexpr (MASKED) {
@@ -828,7 +790,7 @@ __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& 
     if constexpr (TAIL) {
 #pragma unroll
         for (int v = 0; v < 16; ++v)
-            if (padded(v, tcut)) s[v] = kNegInf;
+            if (padded(v, tcut)) s[v] = kNegInf + (MASKED ? 0 : kScoreBias);
     }
     int32_t mx = max3(s[0], s[1], s[2]);
     mx = max3(mx, s[3], s[4]);
@@ -844,11 +806,14 @@ __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& 
 // One 32-key step (qflash/kernel.py:147-174) for the 32 query rows of a wave.
 // Every branch below is wave-uniform and none of them holds an alternative
 // computation of acc (the accumulators keep their registers across steps).
-template <int D, bool MASKED, bool TAIL, bool WIDE, bool DYN, bool FIRST>
+// Scores, m and m' carry the bias SB (kScoreBias when unmasked): only their
+// differences enter the arithmetic.  LUT: LDS address of the p table.
+template <int D, int LUT, bool MASKED, bool TAIL, bool WIDE, bool DYN, bool FIRST>
 __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const i32x4* qv, const int8_t* lk,
                                           const int8_t* lv, const Frag<D>& fr, const BiasRow& brow, int kstart,
-                                          int lane, bool wave_fast, int32_t xlim, int lut_mode, uint32_t lut_base) {
+                                          int lane, bool wave_fast, int32_t xlim, int lut_mode, i32x4 xb) {
     constexpr int DB = D / 32;
+    constexpr int32_t SB = MASKED ? 0 : kScoreBias;
     const int g = lane >> 5;
     const int32_t rs = a.rs, eM = a.eM, rM = a.rM;
 
@@ -856,7 +821,7 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     if constexpr (MASKED) load_bias<TAIL>(bias_v, a, brow, kstart, lane);
     i32x16 s;
     int32_t smin;
-    const int32_t mx = scores<D, MASKED, TAIL>(s, smin, a, qv, lk, fr, bias_v, kstart, lane, lut_mode == 2);
+    const int32_t mx = scores<D, MASKED, TAIL>(s, smin, a, qv, lk, fr, bias_v, kstart, lane, lut_mode == 2, xb);
     const int32_t m = st.m;
     const int32_t mn = max(m, mx);  // kernel.py:158
     const int32_t dm = wsub(m, mn);
@@ -875,12 +840,25 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     uint32_t pk[4];
     i32x4 vf[DB];
     if (lut_ok) {
-        // LDS address of entry min(u, lut_n - 1); u <= lut_lim < 2^31 keeps the sum unwrapped
-        const uint32_t cm = (uint32_t)mn + lut_base, cap = lut_base + (uint32_t)(a.lut_n - 1);
-        uint32_t addr[16];
+        // table index max(s - thr, 0) = lut_n - 1 - min(u, lut_n - 1)
+        const int32_t thr = wsub(mn, a.lut_n - 1);
+        uint32_t idx[16];
+        if constexpr (MASKED) {
+            // s - thr = lut_n - 1 - u >= lut_n - 1 - lut_lim > INT32_MIN: no wrap
 #pragma unroll
-        for (int v = 0; v < 16; ++v) addr[v] = min(cm - (uint32_t)s[v], cap);
-        lut_pack_vt<D>(pk, vf, addr, lv, fr);
+            for (int v = 0; v < 16; ++v) idx[v] = (uint32_t)max(wsub(s[v], thr), 0);
+        } else {
+            // scores and thr in [1, 2^31) (lut_mode != 0 only then): unsigned saturation
+#pragma unroll
+            for (int v = 0; v < 16; ++v) idx[v] = __builtin_elementwise_sub_sat((uint32_t)s[v], (uint32_t)thr);
+            if constexpr (TAIL) {  // padded columns read entry 0 (p = 0); l gets their p below
+                const int32_t tcut = a.N - kstart - 4 * g;
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    if (padded(v, tcut)) idx[v] = 0;
+            }
+        }
+        lut_pack_vt<D, LUT>(pk, vf, idx, lv, fr);
     } else if (vec_ok) {
         // kernel.py:159-161 in six ops per score (see the fast-path comment)
         const int32_t c1 = opaque(wadd(wmul(wsub(0, mn), eM), 1 << 16));
@@ -895,7 +873,7 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
             s[v] = mad24(E, rM, c15);  // p = bits 16..23
         }
         if constexpr (TAIL) {  // padded key columns: p(NEG_INF - m') exactly, once per row
-            const int32_t ppad = (int32_t)((uint32_t)requant(exp2_i32(wsub(kNegInf, mn), a), a) << 16);
+            const int32_t ppad = (int32_t)((uint32_t)requant(exp2_i32(wsub(kNegInf + SB, mn), a), a) << 16);
             const int32_t tcut = a.N - kstart - 4 * g;
 #pragma unroll
             for (int v = 0; v < 16; ++v)
@@ -931,12 +909,10 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     lij = __builtin_amdgcn_sdot4((int)pk[3], 0x01010101, lij, false);
     lij = half_sum(lij);
     if constexpr (TAIL && !MASKED) {
-        // Table path of the last, partial step: a padded column (score NEG_INF)
-        // read entry min(mn - NEG_INF, lut_n - 1), which is its exact p when
-        // mn - NEG_INF <= lut_lim and 0 otherwise; its P.V term is 0 either way
-        // (V rows past N read as 0), so only l needs the padded columns' p then.
-        if (lut_ok && (uint32_t)(mn - kNegInf) > (uint32_t)a.lut_lim)
-            lij = wadd(lij, (32 - (a.N - kstart)) * requant(exp2_i32(wsub(kNegInf, mn), a), a));
+        // Table path of the last, partial step: the padded columns (score
+        // NEG_INF) read p = 0; their P.V term is 0 anyway (V rows past N read
+        // as 0), so only l needs their exact p.
+        if (lut_ok) lij = wadd(lij, (32 - (a.N - kstart)) * requant(exp2_i32(wsub(kNegInf + SB, mn), a), a));
     }
 
     // kernel.py:163-165
@@ -1089,11 +1065,14 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
                                           int q0, bool active, bool wave_fast, int32_t xlim, int lut_mode) {
     using S = Stage<D, W>;
     constexpr int DB = D / 32;
-    const uint32_t lut_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t*)(smem + 2 * S::BYTES);
+    constexpr int LUT = 2 * S::BYTES;  // LDS address of the p table (smem starts at 0)
     FastState<D> st;
 #pragma unroll
     for (int t = 0; t < DB; ++t) st.acc[t] = i32x16{};
-    st.m = kNegInf;  // kernel.py:138
+    st.m = kNegInf + (MASKED ? 0 : kScoreBias);  // kernel.py:138
+    // all bytes -128; opaque to the compiler each step, so that the bias MFMA
+    // is issued per step rather than hoisted into 16 live registers
+    i32x4 xb = i32x4{(int32_t)0x80808080, (int32_t)0x80808080, (int32_t)0x80808080, (int32_t)0x80808080};
     st.l = 1;        // kernel.py:139
     st.bnd = 0.f;
     st.wide = 0;
@@ -1114,8 +1093,8 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
     // step 0 (m = NEG_INF, acc = 0) apart from the loop: the loop body then
     // carries no first-step cases
     if (active && nfull > 0)
-        fast_step<D, MASKED, false, WIDE, DYN, true>(st, a, qv, smem, smem + S::KBYTES, fr, brow, 0, lane, wave_fast,
-                                                     xlim, lut_mode, lut_base);
+        fast_step<D, LUT, MASKED, false, WIDE, DYN, true>(st, a, qv, smem, smem + S::KBYTES, fr, brow, 0, lane,
+                                                          wave_fast, xlim, lut_mode, xb);
     for (int stg = 0; stg < nstage; ++stg) {
         const int8_t* buf = smem + (stg & 1) * S::BYTES;
         if (stg + 1 < nstage) dma.issue(rk, rv, smem + ((stg + 1) & 1) * S::BYTES, (stg + 1) * S::KEYS, a, wave);
@@ -1124,9 +1103,10 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
             for (int half = stg == 0 ? 1 : 0; half < S::STEPS; ++half) {
                 const int step = stg * S::STEPS + half;
                 if (step >= nfull) break;
-                fast_step<D, MASKED, false, WIDE, DYN, false>(st, a, qv, buf + half * 32 * D,
-                                                              buf + S::KBYTES + half * 32 * D, fr, brow, step * 32,
-                                                              lane, wave_fast, xlim, lut_mode, lut_base);
+                if constexpr (!MASKED) asm volatile("" : "+v"(xb));
+                fast_step<D, LUT, MASKED, false, WIDE, DYN, false>(st, a, qv, buf + half * 32 * D,
+                                                                   buf + S::KBYTES + half * 32 * D, fr, brow,
+                                                                   step * 32, lane, wave_fast, xlim, lut_mode, xb);
             }
         }
         stage_sync();
@@ -1137,11 +1117,11 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
         const int8_t* lk = buf + th * 32 * D;
         const int8_t* lv = buf + S::KBYTES + th * 32 * D;
         if (nfull == 0)
-            fast_step<D, MASKED, true, WIDE, DYN, true>(st, a, qv, lk, lv, fr, brow, 0, lane, wave_fast, xlim,
-                                                        lut_mode, lut_base);
+            fast_step<D, LUT, MASKED, true, WIDE, DYN, true>(st, a, qv, lk, lv, fr, brow, 0, lane, wave_fast, xlim,
+                                                             lut_mode, xb);
         else
-            fast_step<D, MASKED, true, WIDE, DYN, false>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane, wave_fast,
-                                                         xlim, lut_mode, lut_base);
+            fast_step<D, LUT, MASKED, true, WIDE, DYN, false>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane,
+                                                              wave_fast, xlim, lut_mode, xb);
     }
     if (!active) return;
     // this wave's 256 bytes of the stage buffer that no step reads any more:
@@ -1165,8 +1145,9 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
     __shared__ __attribute__((aligned(16))) int8_t smem[2 * S::BYTES + kLutMax];
 
     const int tid = threadIdx.x;
-    // p(u) table (lut_pack_vt), visible after fast_rows' first barrier
-    for (int u = tid; u < a.lut_n; u += 64 * W) smem[2 * S::BYTES + u] = (int8_t)requant(exp2_i32(-u, a), a);
+    // p(u) table, entry lut_n - 1 - u (lut_pack_vt), visible after fast_rows' first barrier
+    for (int u = tid; u < a.lut_n; u += 64 * W)
+        smem[2 * S::BYTES + a.lut_n - 1 - u] = (int8_t)requant(exp2_i32(-u, a), a);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int lq = lane & 31, g = lane >> 5;
     const int wg = xcd_order(blockIdx.x, a.n_wg);
@@ -1206,7 +1187,9 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
     // per step.
     bool wave_fast = !a.force_robust;
     int32_t xlim = a.x_safe;
-    int lut_mode = a.lut_n ? 2 : 0;  // 1: u <= lut_lim for every real column, 2: checked per step
+    // the table sits at LDS address 2 * S::BYTES, the byte loads' immediate offset
+    const bool lut_at = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t*)smem == 0;
+    int lut_mode = a.lut_n && lut_at ? 2 : 0;  // 1: u <= lut_lim for every real column, 2: checked per step
     if constexpr (!MASKED) {
         // sum |q|: bytes offset by 128 (xor 0x80) against 0x80 under v_sad_u8
         uint32_t l1u = 0;
@@ -1223,7 +1206,8 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
                         ((X * a.eps_abs + 65535) >> 16) + 2 * (int64_t)a.rs + 1 < (1 << 22);
         wave_fast = wave_fast && __all(ok);
         xlim = (int32_t)(X < (1 << 30) ? X : (1 << 30));
-        if (a.lut_n) lut_mode = __all(X <= a.lut_lim) ? 1 : 2;
+        // biased scores >= kScoreBias - 128 * ||q||_1 > lut_n - 1: scores and thresholds positive
+        if (lut_mode) lut_mode = !__all(X / 2 + kLutMax <= kScoreBias) ? 0 : (__all(X <= a.lut_lim) ? 1 : 2);
     }
 
     // Unmasked waves whose guard holds run a loop that never meets an alpha

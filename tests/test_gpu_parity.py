@@ -234,3 +234,36 @@ def test_table_path_vs_oracle(sm_scale, D, masked, monkeypatch):
     _launch(qd, kd, vd, o, consts, Flags(), None if bias is None else bias.to(DEV))
     torch.cuda.synchronize()
     assert int((o.cpu().numpy() != want).sum()) == 0
+
+
+@pytest.mark.parametrize("sm_scale", [0.05, 1 / 57.3])
+def test_table_path_at_score_bias_edge(sm_scale, monkeypatch):
+    """The unmasked table path takes one saturating subtraction per score,
+    which needs every biased score positive: a wave may use it only while
+    128 * ||q_row||_1 + 4096 <= 2^19 (||q||_1 <= 4064).  Rows of wave 0 sit on
+    that edge (||q||_1 = 4064, keys near -128, so the biased scores come down
+    to 4096), rows of wave 1 one past it (4065: arithmetic path); the spread
+    of the scores in a step stays small, so the steps do take the table."""
+    import ctypes
+    monkeypatch.setenv("QFLASH_HIP_FORCE_LUT", "1")
+    from qflash_amd.kernel import fixed_point_constants
+    consts = Consts(*fixed_point_constants(sm_scale, 30, 30))
+    n, lim = ctypes.c_int32(), ctypes.c_int32()
+    _lib().load().qflash_hip_lut_bounds(consts.sm_rscale, consts.exp_M, consts.req_M, ctypes.byref(n),
+                                        ctypes.byref(lim))
+    print(f"[case] sm_scale={sm_scale} consts={consts} lut=({n.value}, {lim.value})", flush=True)
+    assert n.value > 0
+    g = np.random.default_rng(7)
+    Z, H, N, D = 1, 2, 96, 64
+    q = np.tile(np.array([64, 63] * (D // 2), dtype=np.int64), (Z, H, N, 1))  # ||q||_1 = 4064
+    q[:, :, 32:64, 0] += 1                                                       # 4065
+    assert q.sum(-1).max() == 4065 and 128 * 4064 + 4096 == 1 << 19
+    k = -128 + g.integers(0, 3, (Z, H, N, D))
+    v = g.integers(-128, 128, (Z, H, N, D))
+    q8, k8, v8 = (torch.from_numpy(x.astype(np.int8)) for x in (q, k, v))
+    want = oracle_c.attention_codes(q8, k8, v8, consts, Flags(), threads=8)
+    qd, kd, vd = q8.to(DEV), k8.to(DEV), v8.to(DEV)
+    o = torch.empty_like(vd)
+    _launch(qd, kd, vd, o, consts, Flags())
+    torch.cuda.synchronize()
+    assert int((o.cpu().numpy() != want).sum()) == 0
