@@ -1099,9 +1099,11 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
         const int8_t* buf = smem + (stg & 1) * S::BYTES;
         if (stg + 1 < nstage) dma.issue(rk, rv, smem + ((stg + 1) & 1) * S::BYTES, (stg + 1) * S::KEYS, a, wave);
         if (active) {
-#pragma unroll 1
-            for (int half = stg == 0 ? 1 : 0; half < S::STEPS; ++half) {
+            // unrolled: the steps' LDS offsets within the stage are immediates
+#pragma unroll
+            for (int half = 0; half < S::STEPS; ++half) {
                 const int step = stg * S::STEPS + half;
+                if (half == 0 && stg == 0) continue;  // step 0 ran above
                 if (step >= nfull) break;
                 if constexpr (!MASKED) asm volatile("" : "+v"(xb));
                 fast_step<D, LUT, MASKED, false, WIDE, DYN, false>(st, a, qv, buf + half * 32 * D,
