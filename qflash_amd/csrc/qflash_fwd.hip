@@ -830,10 +830,8 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     if (MASKED || lut_mode == 2) smin = half_min(smin);
     // table path: every real column of the wave has u = m' - s <= lut_lim
     // (lut_mode 1: proved for the whole row block from ||q||_1)
-    bool lut_ok = false;
     // (mn >= smin: the difference is exact as an unsigned 32-bit value)
-    if constexpr (!TAIL || !MASKED)
-        lut_ok = lut_mode == 1 || (lut_mode == 2 && __all((uint32_t)(mn - smin) <= (uint32_t)a.lut_lim));
+    const bool lut_ok = lut_mode == 1 || (lut_mode == 2 && __all((uint32_t)(mn - smin) <= (uint32_t)a.lut_lim));
     bool vec_ok = wave_fast;
     if constexpr (MASKED)
         vec_ok = vec_ok && __all(smin > -(1 << 23) && mn < (1 << 23) && (int64_t)mn - smin <= xlim);
@@ -844,19 +842,19 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
         const int32_t thr = wsub(mn, a.lut_n - 1);
         uint32_t idx[16];
         if constexpr (MASKED) {
-            // s - thr = lut_n - 1 - u >= lut_n - 1 - lut_lim > INT32_MIN: no wrap
+            // real columns: s - thr = lut_n - 1 - u >= lut_n - 1 - lut_lim > INT32_MIN, no wrap
 #pragma unroll
             for (int v = 0; v < 16; ++v) idx[v] = (uint32_t)max(wsub(s[v], thr), 0);
         } else {
             // scores and thr in [1, 2^31) (lut_mode != 0 only then): unsigned saturation
 #pragma unroll
             for (int v = 0; v < 16; ++v) idx[v] = __builtin_elementwise_sub_sat((uint32_t)s[v], (uint32_t)thr);
-            if constexpr (TAIL) {  // padded columns read entry 0 (p = 0); l gets their p below
-                const int32_t tcut = a.N - kstart - 4 * g;
+        }
+        if constexpr (TAIL) {  // padded columns read entry 0 (p = 0); l gets their p below
+            const int32_t tcut = a.N - kstart - 4 * g;
 #pragma unroll
-                for (int v = 0; v < 16; ++v)
-                    if (padded(v, tcut)) idx[v] = 0;
-            }
+            for (int v = 0; v < 16; ++v)
+                if (padded(v, tcut)) idx[v] = 0;
         }
         lut_pack_vt<D, LUT>(pk, vf, idx, lv, fr);
     } else if (vec_ok) {
@@ -908,7 +906,7 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     lij = __builtin_amdgcn_sdot4((int)pk[2], 0x01010101, lij, false);
     lij = __builtin_amdgcn_sdot4((int)pk[3], 0x01010101, lij, false);
     lij = half_sum(lij);
-    if constexpr (TAIL && !MASKED) {
+    if constexpr (TAIL) {
         // Table path of the last, partial step: the padded columns (score
         // NEG_INF) read p = 0; their P.V term is 0 anyway (V rows past N read
         // as 0), so only l needs their exact p.
@@ -1147,9 +1145,11 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
     __shared__ __attribute__((aligned(16))) int8_t smem[2 * S::BYTES + kLutMax];
 
     const int tid = threadIdx.x;
-    // p(u) table, entry lut_n - 1 - u (lut_pack_vt), visible after fast_rows' first barrier
+    // p(u) table, entry lut_n - 1 - u (lut_pack_vt), visible after fast_rows'
+    // first barrier; lut_n - 1 <= x_safe (host), where the 24-bit E is exact
     for (int u = tid; u < a.lut_n; u += 64 * W)
-        smem[2 * S::BYTES + a.lut_n - 1 - u] = (int8_t)requant(exp2_i32(-u, a), a);
+        smem[2 * S::BYTES + a.lut_n - 1 - u] =
+            (int8_t)(mad24(exp2_fast(-u, a.eM, a.rs), a.rM, 1 << 15) >> 16);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int lq = lane & 31, g = lane >> 5;
     const int wg = xcd_order(blockIdx.x, a.n_wg);
@@ -1365,10 +1365,13 @@ static void choose_lut(Args& a, int W) {
     a.lut_n = 0;
     a.lut_lim = 0;
     if (a.force_robust || getenv_flag("QFLASH_HIP_NO_LUT")) return;  // test hooks
-    const bool pays = a.N >= 128 && (int64_t)a.n_wg * W >= 8192;
+    // the table replaces ~80 VALU instructions per 32-key step, and filling it
+    // costs each wave ~10 per 64 * W entries
+    const bool pays = a.N >= 32;
     if (!pays && !getenv_flag("QFLASH_HIP_FORCE_LUT")) return;
     int32_t n, lim;
     lut_bounds(a, &n, &lim);
+    if (n - 1 > a.x_safe) return;  // the kernel fills the table with the 24-bit E
     a.lut_n = n;
     a.lut_lim = lim;
 }
