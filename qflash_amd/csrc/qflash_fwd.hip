@@ -759,13 +759,16 @@ __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& 
                                           const int8_t* lk, const Frag<D>& fr, const int32_t* bias_v, int kstart,
                                           int lane, bool need_min, i32x4 xb) {
     constexpr int DB = D / 32;
-    s = i32x16{};
+    // K fragments first: the bias MFMA runs while they are in flight
+    i32x4 kf[DB];
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-        const i32x4 kf = *reinterpret_cast<const i32x4*>(lk + fr.k[db]);
-        s = mfma32(kf, qv[db], s);
-    }
-    if constexpr (!MASKED) s = mfma32(xb, xb, s);
+    for (int db = 0; db < DB; ++db) kf[db] = *reinterpret_cast<const i32x4*>(lk + fr.k[db]);
+    if constexpr (MASKED)
+        s = i32x16{};
+    else
+        s = mfma32(xb, xb, i32x16{});
+#pragma unroll
+    for (int db = 0; db < DB; ++db) s = mfma32(kf[db], qv[db], s);
     smin = INT32_MAX;
     const int32_t tcut = a.N - kstart - 4 * (lane >> 5);
     if constexpr (MASKED) {
