@@ -830,7 +830,10 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     const int32_t dm = wsub(m, mn);
     constexpr bool first = FIRST;  // kstart == 0
 
-    if (MASKED || lut_mode == 2) smin = half_min(smin);
+    // Each lane half checks its own minimum against the row's mn (the checks
+    // below are wave-wide); a masked partial step's half may have no real
+    // column (minimum INT32_MAX) and takes the other half's.
+    if constexpr (MASKED && TAIL) smin = half_min(smin);
     // table path: every real column of the wave has u = m' - s <= lut_lim
     // (lut_mode 1: proved for the whole row block from ||q||_1)
     // (mn >= smin: the difference is exact as an unsigned 32-bit value)
