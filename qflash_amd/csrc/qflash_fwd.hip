@@ -74,8 +74,8 @@ struct Args {
     int32_t n_wg;    // workgroups in the grid (XCD-aware order)
     int32_t bias_zmod;  // > 0: the bias of batch index z is bias[z % bias_zmod] (window-periodic)
     int32_t bias_vec;   // bias rows have unit key stride and non-negative strides: 16-byte buffer loads
-    // exp2 + requantisation by table (see lut_pack_vt): p(u) = lut[min(u, lut_n - 1)]
-    // for u = m' - s in [0, lut_lim]
+    // exp2 + requantisation by table (see lut_pack_vt): p(u) = p(min(u, lut_n - 1))
+    // for u = m' - s in [0, lut_lim], the table holding p(0 .. lut_n - 1) in reverse
     int32_t lut_n;      // table entries (the last one 0), 0 = no table
     int32_t lut_lim;
     // output: int8 codes at `o` (out_dt == QFLASH_HIP_I8), or RN_T(code * o_scale)
