@@ -267,3 +267,32 @@ def test_table_path_at_score_bias_edge(sm_scale, monkeypatch):
     _launch(qd, kd, vd, o, consts, Flags())
     torch.cuda.synchronize()
     assert int((o.cpu().numpy() != want).sum()) == 0
+
+
+@pytest.mark.parametrize("masked", [False, True])
+@pytest.mark.parametrize("D", [32, 64])
+@pytest.mark.parametrize("N", [33, 36, 37, 49, 68])
+def test_table_path_short_tails(N, D, masked, monkeypatch):
+    """Partial last steps of 1-5 keys (the upper lane half of the step has no
+    real column up to 4) and 17 keys, on the table path, masked or not: the
+    padded columns read entry 0 and l gets their exact p; small score spreads
+    and a small bias keep every step on the table."""
+    monkeypatch.setenv("QFLASH_HIP_FORCE_LUT", "1")
+    from qflash_amd.kernel import fixed_point_constants
+    consts = Consts(*fixed_point_constants(1 / 57.3, 30, 30))
+    print(f"[case] N={N} D={D} masked={masked}", flush=True)
+    g = np.random.default_rng(N * 7 + D + masked)
+    Z, H = 2, 3
+    q = np.clip(np.rint(g.standard_normal((Z, H, N, D)) * 4), -128, 127)
+    k = np.clip(np.rint(g.standard_normal((Z, H, N, D)) * 4), -128, 127)
+    v = g.integers(-128, 128, (Z, H, N, D))
+    q8, k8, v8 = (torch.from_numpy(x.astype(np.int8)) for x in (q, k, v))
+    bias = None
+    if masked:
+        bias = torch.from_numpy(g.integers(-40, 41, (Z, H, N, N)).astype(np.int32))
+    want = oracle_c.attention_codes(q8, k8, v8, consts, Flags(), bias=bias, threads=8)
+    qd, kd, vd = q8.to(DEV), k8.to(DEV), v8.to(DEV)
+    o = torch.empty_like(vd)
+    _launch(qd, kd, vd, o, consts, Flags(), None if bias is None else bias.to(DEV))
+    torch.cuda.synchronize()
+    assert int((o.cpu().numpy() != want).sum()) == 0
