@@ -296,3 +296,39 @@ def test_table_path_short_tails(N, D, masked, monkeypatch):
     _launch(qd, kd, vd, o, consts, Flags(), None if bias is None else bias.to(DEV))
     torch.cuda.synchronize()
     assert int((o.cpu().numpy() != want).sum()) == 0
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_random_shapes_vs_oracle(case, monkeypatch):
+    """Seeded random shapes, scales, code spreads and biases through every
+    fast-kernel path (table or not, masked or not, partial steps), bit-exact
+    against the C oracle."""
+    from qflash_amd.kernel import fixed_point_constants
+    g = np.random.default_rng(1000 + case)
+    N = int(g.integers(1, 300))
+    D = int(g.choice([32, 64, 128]))
+    Z, H = int(g.integers(1, 3)), int(g.integers(1, 4))
+    sm = float(g.choice([1 / 3.4, 1 / 8, 0.05, 1 / 57.3, 0.0123, 1 / 94.2]))
+    spread = float(g.choice([2.0, 8.0, 30.0, 90.0]))
+    masked = bool(case % 3 == 0)
+    if case % 2:
+        monkeypatch.setenv("QFLASH_HIP_FORCE_LUT", "1")
+    consts = Consts(*fixed_point_constants(sm, 30, 30))
+    print(f"[case] {case}: Z={Z} H={H} N={N} D={D} sm={sm:.4f} spread={spread} masked={masked} "
+          f"force_lut={case % 2}", flush=True)
+    q = np.clip(np.rint(g.standard_normal((Z, H, N, D)) * spread), -128, 127)
+    k = np.clip(np.rint(g.standard_normal((Z, H, N, D)) * spread), -128, 127)
+    v = g.integers(-128, 128, (Z, H, N, D))
+    q8, k8, v8 = (torch.from_numpy(x.astype(np.int8)) for x in (q, k, v))
+    bias = None
+    if masked:
+        lim = int(g.choice([4, 300, 1 << 20]))
+        b = g.integers(-lim, lim + 1, (Z, H, N, N))
+        b[g.random((Z, H, N, N)) < 0.2] = -(1 << 20)
+        bias = torch.from_numpy(b.astype(np.int32))
+    want = oracle_c.attention_codes(q8, k8, v8, consts, Flags(), bias=bias, threads=8)
+    qd, kd, vd = q8.to(DEV), k8.to(DEV), v8.to(DEV)
+    o = torch.empty_like(vd)
+    _launch(qd, kd, vd, o, consts, Flags(), None if bias is None else bias.to(DEV))
+    torch.cuda.synchronize()
+    assert int((o.cpu().numpy() != want).sum()) == 0
