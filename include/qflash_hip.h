@@ -121,6 +121,22 @@ int qflash_hip_quantize(const void* q, const void* k, const void* v, int32_t dty
                         void* stream);
 
 /*
+ * int32 logit bias of QWindowAttention's mask, replacing the torch ops that
+ * build it: the sum rel + mask of qflash/attention.py:68-74 (on the n_win
+ * distinct slices, as qflash_hip_window_kernel reads them) followed by the
+ * float-mask conversion of qflash/kernel.py:327-336, in one pass:
+ *   x = RN_fp32(rel[h, i, j] + mask[w, i, j])   (mask NULL: x = rel[h, i, j], n_win = 1)
+ *   out[w, h, i, j] = -2^20                                          if x < -100
+ *                   = (int32) rint(RN_fp32(RN_fp32(x * L) * R))      otherwise,
+ * L = RN_fp32(1.44269504), R = RN_fp32(1 / RN_fp32(sm_scale)): torch's
+ * arithmetic on the GPU for x * LOG2E / sm_scale with host scalars.
+ * rel: (H, N, N), mask: (n_win, N, N), out: (n_win, H, N, N), all contiguous
+ * device memory.  Allocates nothing; asynchronous on `stream`.
+ */
+int qflash_hip_window_bias(const float* rel, const float* mask, int32_t n_win, int32_t H, int32_t N,
+                           double sm_scale, int32_t* out, void* stream);
+
+/*
  * One entry point for every case of the forward, used by qflash_forward: the
  * masks of both masked entries (attn_bias NULL = unmasked; bias_zmod 0 = the
  * bias has Z slices, > 0 = window-periodic as in qflash_hip_window_kernel),

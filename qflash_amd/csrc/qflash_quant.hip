@@ -39,6 +39,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kThreads = 256;
 constexpr int kSeg = 8 * kThreads;  // 16-byte chunks per work unit
 constexpr int kSlots = 64;          // atomic-max slots per tensor (spreads the contention)
+constexpr int32_t kNegInfBias = -(1 << 20);  // qflash/kernel.py:288
 static_assert(3 * kSlots <= QFLASH_HIP_SCALES_WORKSPACE, "workspace: 3 x kSlots partial maxima");
 
 // One tensor as `rows` runs of L contiguous elements; a run's start is
@@ -454,6 +455,25 @@ static int quant_dt(Geo* g, const void* scales, hipStream_t st) {
     return e == hipSuccess ? 0 : fail(QFLASH_HIP_ELAUNCH, "launch failed: %s", hipGetErrorString(e));
 }
 
+// int32 bias of a window mask (qflash_hip_window_bias): one element per
+// thread, the torch ops' fp32 roundings in their order (an add, the compare
+// with -100, two products by the host scalars RN(LOG2E) and RN(1/sm_scale) --
+// torch multiplies by the reciprocal of a host-scalar divisor -- round half to
+// even, conversion).
+__global__ __launch_bounds__(256) void window_bias_kernel(const float* rel, const float* mask, int32_t H,
+                                                           int32_t nn, int64_t total, float log2e, float inv_sm,
+                                                           int32_t* out) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= total) return;
+    const int64_t ij = e % nn, wh = e / nn;
+    const int64_t h = wh % H, w = wh / H;
+    float x = rel[h * nn + ij];
+    if (mask) x = __fadd_rn(x, mask[w * nn + ij]);
+    const bool masked = x < -100.0f;
+    const float y = __fmul_rn(__fmul_rn(masked ? 0.0f : x, log2e), inv_sm);
+    out[e] = masked ? kNegInfBias : (int32_t)rintf(y);
+}
+
 static int esize_of(int32_t dtype) {
     return dtype == QFLASH_HIP_F32 ? 4 : (dtype == QFLASH_HIP_F16 || dtype == QFLASH_HIP_BF16 ? 2 : 0);
 }
@@ -507,6 +527,27 @@ int qflash_hip_quantize(const void* q, const void* k, const void* v, int32_t dty
         case QFLASH_HIP_F16: return qfq::quant_dt<QFLASH_HIP_F16>(g, scales, st);
         default: return qfq::quant_dt<QFLASH_HIP_BF16>(g, scales, st);
     }
+}
+
+int qflash_hip_window_bias(const float* rel, const float* mask, int32_t n_win, int32_t H, int32_t N,
+                           double sm_scale, int32_t* out, void* stream) {
+    qfq::g_err[0] = 0;
+    if (!rel || !out) return qfq::fail(QFLASH_HIP_EINVAL, "null pointer argument");
+    if (H <= 0 || N <= 0 || n_win <= 0 || (!mask && n_win != 1))
+        return qfq::fail(QFLASH_HIP_EINVAL, "bad window bias shape nW=%d H=%d N=%d%s", n_win, H, N,
+                         mask ? "" : " (no mask: nW must be 1)");
+    if (!(sm_scale > 0.0) || !(sm_scale < 1e30)) return qfq::fail(QFLASH_HIP_EINVAL, "bad sm_scale %g", sm_scale);
+    const int64_t nn = (int64_t)N * N, total = (int64_t)n_win * H * nn;
+    if (total >= ((int64_t)1 << 31)) return qfq::fail(QFLASH_HIP_EINVAL, "window bias too large");
+    // torch: x * LOG2E and x / sm_scale with host scalars, both taken to fp32
+    // (the division as a product with the fp32 reciprocal of the fp32 divisor)
+    const float log2e = (float)1.44269504;
+    const float inv_sm = 1.0f / (float)sm_scale;
+    hipLaunchKernelGGL(qfq::window_bias_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, rel, mask, H, (int32_t)nn, total, log2e, inv_sm, out);
+    if (hipError_t err = hipGetLastError(); err != hipSuccess)
+        return qfq::fail(QFLASH_HIP_ELAUNCH, "window bias launch: %s", hipGetErrorString(err));
+    return 0;
 }
 
 }  // extern "C"

@@ -82,6 +82,31 @@ def bias_values(attn_mask: Tensor, sm_scale: float) -> Tensor:
     return quant.masked_fill(is_masked, NEG_INF)
 
 
+def window_bias(rel_bias: Tensor, mask: Tensor | None, sm_scale: float) -> Tensor:
+    """bias_values(rel_bias + mask.view(nW, 1, N, N), sm_scale) (or of rel_bias
+    alone when mask is None) as a contiguous (nW or 1, H, N, N) int32 tensor.
+
+    fp32 inputs on the device take qflash_hip_window_bias (one pass instead
+    of the eight torch kernels, same values); other dtypes keep the torch
+    ops, whose arithmetic is in the mask's dtype.
+    """
+    H, N = rel_bias.shape[-3], rel_bias.shape[-1]
+    fp32 = rel_bias.dtype == torch.float32 and (mask is None or mask.dtype == torch.float32)
+    if not (fp32 and rel_bias.is_cuda and (mask is None or mask.is_cuda)):
+        x = rel_bias.reshape(1, H, N, N) if mask is None else rel_bias + mask.view(mask.shape[0], 1, N, N)
+        return bias_values(x, sm_scale).contiguous()
+    rel = rel_bias.reshape(H, N, N).contiguous()
+    m = None if mask is None else mask.contiguous()
+    n_win = 1 if m is None else m.shape[0]
+    out = torch.empty((n_win, H, N, N), dtype=torch.int32, device=rel.device)
+    L = _lib.load()
+    _lib.check(L.qflash_hip_window_bias(ctypes.c_void_p(rel.data_ptr()),
+                                        ctypes.c_void_p(0 if m is None else m.data_ptr()), n_win, H, N,
+                                        float(sm_scale), ctypes.c_void_p(out.data_ptr()), _stream_ptr(rel)),
+               "qflash_hip_window_bias")
+    return out
+
+
 def mask_to_bias(attn_mask: Tensor, sm_scale: float, Z: int, H: int, N: int, materialize: bool = False) -> Tensor:
     """Boolean or float mask -> int32 logit bias of shape (Z, H, N, N), kernel.py:327-336.
 
@@ -416,12 +441,12 @@ def qflash_forward_window(query: Tensor, key: Tensor, value: Tensor, rel_bias: T
     flag_kw = dict(EXP_USE_SHIFT=EXP_USE_SHIFT, L_USE_SHIFT=L_USE_SHIFT, ACC_USE_SHIFT=ACC_USE_SHIFT,
                    L_SHIFT=L_SHIFT, ACC_SHIFT=ACC_SHIFT)
     if mask is None:
-        bias, zmod = mask_to_bias(rel_bias, sm_scale, Z, H, N), 0
+        bias, zmod = window_bias(rel_bias, None, sm_scale).expand(Z, H, N, N), 0
     else:
         n_win = mask.shape[0]
         if Z % n_win:
             raise ValueError(f"batch {Z} is not a multiple of the {n_win} windows of the mask")
-        bias, zmod = bias_values(rel_bias + mask.view(n_win, 1, N, N), sm_scale).contiguous(), n_win
+        bias, zmod = window_bias(rel_bias, mask, sm_scale), n_win
     if o_scale.dtype in _DT_CODE:  # o * o_scale fused into the kernel's stores
         out = torch.empty_like(v8, dtype=o_scale.dtype)
         launch_forward(q8, k8, v8, out, consts, flag_kw, bias, zmod, o_scale=o_scale)

@@ -1,0 +1,68 @@
+"""qflash_hip_window_bias against the torch ops it replaces (GPU).
+
+The reference builds QWindowAttention's int32 bias with torch ops on the
+device (qflash/attention.py:68-74, then qflash/kernel.py:327-336);
+`bias_values` restates them op for op.  The fused kernel must give the same
+int32 for every element: random tables and masks, values on both sides of the
+-100 threshold, and products near half-integers, where the order of the fp32
+roundings decides the result.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from qflash_amd.kernel import bias_values, window_bias
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _torch_bias(rel, mask, sm):
+    H, N = rel.shape[-3], rel.shape[-1]
+    x = rel.reshape(1, H, N, N) if mask is None else rel + mask.view(mask.shape[0], 1, N, N)
+    return bias_values(x, sm).contiguous()
+
+
+@pytest.mark.parametrize("sm", [0.1767766952966369 * 1.4426950408889634, 0.05, 1 / 57.3, 0.9, 3.7])
+@pytest.mark.parametrize("with_mask", [False, True])
+def test_window_bias_matches_torch_ops(sm, with_mask):
+    print(f"[case] sm={sm} with_mask={with_mask}", flush=True)
+    g = np.random.default_rng(int(sm * 1e4) + with_mask)
+    H, N, nW = 3, 49, 16
+    rel = torch.from_numpy((g.standard_normal((1, H, N, N)) * 0.02).astype(np.float32)).to(DEV)
+    mask = None
+    if with_mask:
+        m = np.zeros((nW, N, N), np.float32)
+        m[g.random((nW, N, N)) < 0.3] = -100.0
+        edge = g.random((nW, N, N))
+        m[edge < 0.05] = np.float32(-99.99999)
+        m[(edge >= 0.05) & (edge < 0.1)] = np.float32(-100.00001)
+        m[(edge >= 0.1) & (edge < 0.15)] = -1e9
+        mask = torch.from_numpy(m).to(DEV)
+    got = window_bias(rel, mask, sm)
+    want = _torch_bias(rel, mask, sm)
+    torch.cuda.synchronize()
+    assert got.shape == want.shape and got.dtype == torch.int32
+    assert int((got != want).sum()) == 0
+
+
+@pytest.mark.parametrize("sm", [0.05, 1 / 57.3, 0.3])
+def test_window_bias_at_rounding_boundaries(sm):
+    """x * LOG2E / sm_scale within a few ulp of k + 1/2 for many k."""
+    print(f"[case] sm={sm}", flush=True)
+    H, N = 2, 64
+    k = np.arange(-2000, 2000, dtype=np.float64)
+    target = (k + 0.5) * sm / 1.44269504
+    x = np.concatenate([np.nextafter(target.astype(np.float32), np.float32(np.inf)),
+                        target.astype(np.float32),
+                        np.nextafter(target.astype(np.float32), np.float32(-np.inf))])
+    x = x[np.abs(x) < 90.0]
+    flat = np.resize(x, H * N * N).astype(np.float32)
+    rel = torch.from_numpy(flat.reshape(1, H, N, N)).to(DEV)
+    for mask in (None, torch.zeros((4, N, N), dtype=torch.float32, device=DEV)):
+        got = window_bias(rel, mask, sm)
+        want = _torch_bias(rel, mask, sm)
+        torch.cuda.synchronize()
+        assert int((got != want).sum()) == 0
