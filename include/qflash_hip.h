@@ -137,6 +137,13 @@ int qflash_hip_window_bias(const float* rel, const float* mask, int32_t n_win, i
                            double sm_scale, int32_t* out, void* stream);
 
 /*
+ * The same conversion for a float attn_mask of any shape (qflash/kernel.py:
+ * 327-336, the fp32 case of bias_values), element for element over n
+ * contiguous fp32 values: one pass instead of the torch ops' eight.
+ */
+int qflash_hip_mask_bias(const float* mask, int64_t n, double sm_scale, int32_t* out, void* stream);
+
+/*
  * One entry point for every case of the forward, used by qflash_forward: the
  * masks of both masked entries (attn_bias NULL = unmasked; bias_zmod 0 = the
  * bias has Z slices, > 0 = window-periodic as in qflash_hip_window_kernel),

@@ -32,7 +32,8 @@ class Flags(ctypes.Structure):
 
 EXPORTS = ("qflash_hip_kernel", "qflash_hip_masked_kernel", "qflash_hip_window_kernel", "qflash_hip_forward",
            "qflash_hip_scales",
-           "qflash_hip_quantize", "qflash_hip_window_bias", "qflash_hip_last_error",
+           "qflash_hip_quantize", "qflash_hip_window_bias", "qflash_hip_mask_bias",
+           "qflash_hip_last_error",
            "qflash_hip_mfma_layout_check", "qflash_hip_lut_bounds", "qflash_hip_version")
 
 # element type codes of qflash_hip_scales / qflash_hip_quantize, and its workspace
@@ -62,6 +63,8 @@ def _declare(L):
     L.qflash_hip_quantize.argtypes = [vp, vp, vp, i32, i64p, vp, vp, vp, i64p, vp, vp]
     L.qflash_hip_window_bias.restype = ctypes.c_int
     L.qflash_hip_window_bias.argtypes = [vp, vp, i32, i32, i32, ctypes.c_double, vp, vp]
+    L.qflash_hip_mask_bias.restype = ctypes.c_int
+    L.qflash_hip_mask_bias.argtypes = [vp, ctypes.c_int64, ctypes.c_double, vp, vp]
     L.qflash_hip_forward.restype = ctypes.c_int
     L.qflash_hip_forward.argtypes = [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32, i32, i32, i64p, i32, i32, i32,
                                      i32, fp, vp]

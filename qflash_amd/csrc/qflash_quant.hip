@@ -550,4 +550,18 @@ int qflash_hip_window_bias(const float* rel, const float* mask, int32_t n_win, i
     return 0;
 }
 
+int qflash_hip_mask_bias(const float* mask, int64_t n, double sm_scale, int32_t* out, void* stream) {
+    qfq::g_err[0] = 0;
+    if (!mask || !out) return qfq::fail(QFLASH_HIP_EINVAL, "null pointer argument");
+    if (n <= 0 || n >= ((int64_t)1 << 31)) return qfq::fail(QFLASH_HIP_EINVAL, "bad mask size %lld", (long long)n);
+    if (!(sm_scale > 0.0) || !(sm_scale < 1e30)) return qfq::fail(QFLASH_HIP_EINVAL, "bad sm_scale %g", sm_scale);
+    const float log2e = (float)1.44269504;
+    const float inv_sm = 1.0f / (float)sm_scale;
+    hipLaunchKernelGGL(qfq::window_bias_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, mask, nullptr, 1, (int32_t)n, n, log2e, inv_sm, out);
+    if (hipError_t err = hipGetLastError(); err != hipSuccess)
+        return qfq::fail(QFLASH_HIP_ELAUNCH, "mask bias launch: %s", hipGetErrorString(err));
+    return 0;
+}
+
 }  // extern "C"

@@ -114,7 +114,16 @@ def mask_to_bias(attn_mask: Tensor, sm_scale: float, Z: int, H: int, N: int, mat
     view (stride 0 on broadcast dims) instead of a materialised copy, which
     the kernels read through their strides.
     """
-    bias = bias_values(attn_mask, sm_scale).expand(Z, H, N, N)
+    if attn_mask.dtype == torch.float32 and attn_mask.is_cuda and 0 < attn_mask.numel() < (1 << 31):
+        # one HIP pass (qflash_hip_mask_bias) with the values of bias_values' torch ops
+        m = attn_mask.contiguous()
+        b = torch.empty(m.shape, dtype=torch.int32, device=m.device)
+        _lib.check(_lib.load().qflash_hip_mask_bias(ctypes.c_void_p(m.data_ptr()), m.numel(), float(sm_scale),
+                                                    ctypes.c_void_p(b.data_ptr()), _stream_ptr(m)),
+                   "qflash_hip_mask_bias")
+    else:
+        b = bias_values(attn_mask, sm_scale)
+    bias = b.expand(Z, H, N, N)
     return bias.contiguous() if materialize else bias
 
 

@@ -66,3 +66,24 @@ def test_window_bias_at_rounding_boundaries(sm):
         want = _torch_bias(rel, mask, sm)
         torch.cuda.synchronize()
         assert int((got != want).sum()) == 0
+
+
+@pytest.mark.parametrize("shape", [(49, 49), (1, 3, 49, 49), (8, 3, 49, 49)])
+def test_mask_bias_matches_torch_ops(shape):
+    """qflash_hip_mask_bias (mask_to_bias on an fp32 device mask) against
+    bias_values' torch ops, with values at and around the -100 threshold."""
+    from qflash_amd.kernel import mask_to_bias
+    print(f"[case] shape={shape}", flush=True)
+    g = np.random.default_rng(len(shape) * 100 + shape[0])
+    m = (g.standard_normal(shape) * 3).astype(np.float32)
+    sel = g.random(shape)
+    m[sel < 0.2] = -100.0
+    m[(sel >= 0.2) & (sel < 0.25)] = np.float32(-99.99999)
+    m[(sel >= 0.25) & (sel < 0.3)] = -1e30
+    mask = torch.from_numpy(m).to(DEV)
+    sm = 0.1767766952966369 * 1.4426950408889634
+    Z, H, N = 8, 3, 49
+    got = mask_to_bias(mask, sm, Z, H, N, materialize=True)
+    want = bias_values(mask, sm).expand(Z, H, N, N).contiguous()
+    torch.cuda.synchronize()
+    assert int((got != want).sum()) == 0
