@@ -217,10 +217,10 @@ def run_config(name: str, steps: int, warmup: int, dev, seed: int = 0, cpu: bool
     return res
 
 
-def e2e_us(w, dev, reps: int = 10) -> float:
-    """Median wall time of the whole op on fp inputs already on the device:
-    qflash.forward (scales, the host sync, constants, quantisation, bias,
-    kernel, dequantisation), or QWindowAttention's call for Swin configs."""
+def e2e_call(w, dev):
+    """The whole op on fp inputs already on the device: qflash.forward (scales,
+    the host sync, constants, quantisation, bias, kernel, dequantisation), or
+    QWindowAttention's call for Swin configs."""
     import torch
 
     from qflash_amd import qflash
@@ -242,6 +242,14 @@ def e2e_us(w, dev, reps: int = 10) -> float:
 
         def call():
             return qflash.forward(q, k, v, attn_mask=mask)
+    return call
+
+
+def e2e_us(w, dev, reps: int = 10) -> float:
+    """Median wall time of e2e_call, host sync included."""
+    import torch
+
+    call = e2e_call(w, dev)
     call()
     torch.cuda.synchronize()
     times = []
@@ -267,6 +275,10 @@ def main(argv=None):
                     help="only the timed kernel launches (for rocprofv3 counter runs)")
     ap.add_argument("--shape", default=None, metavar="Z,H,N,D",
                     help="with --profile: cfg3-distributed inputs of this shape instead of --config")
+    ap.add_argument("--profile-e2e", action="store_true",
+                    help="only the end-to-end op (warmup + steps calls, synchronised each) for rocprofv3 runs")
+    ap.add_argument("--dense-bias", action="store_true",
+                    help="with --profile-e2e on a Swin config: the materialised (B_, H, N, N) mask path")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
                     help="run 10 plain device copies of MB MiB (HBM counter calibration) and exit")
     args = ap.parse_args(argv)
@@ -290,6 +302,19 @@ def main(argv=None):
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes": n, "copies": 10}), flush=True)
+        return 0
+    if args.profile_e2e:
+        w = prepare(args.config, args.seed, dev, dense_bias=args.dense_bias)
+        call = e2e_call(w, dev)
+        times = []
+        for i in range(args.warmup + args.steps):
+            t = time.perf_counter()
+            call()
+            torch.cuda.synchronize()
+            if i >= args.warmup:
+                times.append((time.perf_counter() - t) * 1e6)
+        print(json.dumps({"config": args.config, "dense_bias": args.dense_bias, "steps": args.steps,
+                          "e2e_us_median": statistics.median(times)}), flush=True)
         return 0
     if args.profile:
         if args.shape:

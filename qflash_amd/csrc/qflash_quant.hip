@@ -460,18 +460,37 @@ static int quant_dt(Geo* g, const void* scales, hipStream_t st) {
 // with -100, two products by the host scalars RN(LOG2E) and RN(1/sm_scale) --
 // torch multiplies by the reciprocal of a host-scalar divisor -- round half to
 // even, conversion).
+__device__ __forceinline__ int32_t bias_of(float x, float log2e, float inv_sm) {
+    const bool masked = x < -100.0f;
+    const float y = __fmul_rn(__fmul_rn(masked ? 0.0f : x, log2e), inv_sm);
+    return masked ? kNegInfBias : (int32_t)rintf(y);
+}
+
 __global__ __launch_bounds__(256) void window_bias_kernel(const float* rel, const float* mask, int32_t H,
                                                            int32_t nn, int64_t total, float log2e, float inv_sm,
                                                            int32_t* out) {
     const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (e >= total) return;
-    const int64_t ij = e % nn, wh = e / nn;
-    const int64_t h = wh % H, w = wh / H;
-    float x = rel[h * nn + ij];
-    if (mask) x = __fadd_rn(x, mask[w * nn + ij]);
-    const bool masked = x < -100.0f;
-    const float y = __fmul_rn(__fmul_rn(masked ? 0.0f : x, log2e), inv_sm);
-    out[e] = masked ? kNegInfBias : (int32_t)rintf(y);
+    const int32_t ij = (int32_t)(e % nn), wh = (int32_t)(e / nn);
+    const int32_t h = wh % H, w = wh / H;
+    float x = rel[(int64_t)h * nn + ij];
+    if (mask) x = __fadd_rn(x, mask[(int64_t)w * nn + ij]);
+    out[e] = bias_of(x, log2e, inv_sm);
+}
+
+// qflash_hip_mask_bias: four elements per thread, 16-byte loads and stores
+// when both buffers are 16-byte aligned.
+__global__ __launch_bounds__(256) void mask_bias_kernel(const float* mask, int64_t n, bool vec, float log2e,
+                                                         float inv_sm, int32_t* out) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (vec && i + 4 <= n) {
+        const float4 x = *reinterpret_cast<const float4*>(mask + i);
+        *reinterpret_cast<int4*>(out + i) = int4{bias_of(x.x, log2e, inv_sm), bias_of(x.y, log2e, inv_sm),
+                                                 bias_of(x.z, log2e, inv_sm), bias_of(x.w, log2e, inv_sm)};
+    } else {
+        for (int j = 0; j < 4; ++j)
+            if (i + j < n) out[i + j] = bias_of(mask[i + j], log2e, inv_sm);
+    }
 }
 
 static int esize_of(int32_t dtype) {
@@ -557,8 +576,9 @@ int qflash_hip_mask_bias(const float* mask, int64_t n, double sm_scale, int32_t*
     if (!(sm_scale > 0.0) || !(sm_scale < 1e30)) return qfq::fail(QFLASH_HIP_EINVAL, "bad sm_scale %g", sm_scale);
     const float log2e = (float)1.44269504;
     const float inv_sm = 1.0f / (float)sm_scale;
-    hipLaunchKernelGGL(qfq::window_bias_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                       (hipStream_t)stream, mask, nullptr, 1, (int32_t)n, n, log2e, inv_sm, out);
+    const bool vec = (((uintptr_t)mask | (uintptr_t)out) & 15u) == 0;
+    hipLaunchKernelGGL(qfq::mask_bias_kernel, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0,
+                       (hipStream_t)stream, mask, n, vec, log2e, inv_sm, out);
     if (hipError_t err = hipGetLastError(); err != hipSuccess)
         return qfq::fail(QFLASH_HIP_ELAUNCH, "mask bias launch: %s", hipGetErrorString(err));
     return 0;

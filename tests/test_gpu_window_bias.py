@@ -87,3 +87,24 @@ def test_mask_bias_matches_torch_ops(shape):
     want = bias_values(mask, sm).expand(Z, H, N, N).contiguous()
     torch.cuda.synchronize()
     assert int((got != want).sum()) == 0
+
+
+def test_mask_bias_unaligned_and_ragged():
+    """A mask whose data starts 4 bytes into its buffer (scalar path) and
+    sizes that are not multiples of 4 (the last partial group)."""
+    import ctypes
+
+    from qflash_amd.kernel import _lib as lib, _stream_ptr
+    g = np.random.default_rng(5)
+    base = torch.from_numpy((g.standard_normal(1 + 7 * 49) * 40).astype(np.float32)).to(DEV)
+    mask = base[1:].view(7, 49)                   # 4-byte offset into the allocation
+    assert mask.data_ptr() % 16 != 0 and mask.is_contiguous()
+    sm = 0.3
+    for m in (mask, base[:343].view(7, 49), base[:341]):
+        out = torch.empty(m.shape, dtype=torch.int32, device=DEV)
+        rc = lib.load().qflash_hip_mask_bias(ctypes.c_void_p(m.data_ptr()), m.numel(), sm,
+                                             ctypes.c_void_p(out.data_ptr()), _stream_ptr(m))
+        lib.check(rc, "qflash_hip_mask_bias")
+        want = bias_values(m, sm)
+        torch.cuda.synchronize()
+        assert int((out != want).sum()) == 0
