@@ -412,14 +412,19 @@ static int make_geo(Geo& g, const void* p, const int64_t* n4, const int64_t* s4,
     return 0;
 }
 
-// Blocks per tensor.  flat: `cpt` 16-byte chunks per thread (measured on MI355X
-// at 113 MB per tensor: the absmax pass, which ends each block with an atomic,
-// is fastest at QF_ABSMAX_CPT, the quantisation pass at QF_QUANT_CPT).
+// Blocks per tensor.  flat: `cpt` 16-byte chunks per thread, but at least
+// QF_MIN_BLOCKS blocks (measured on MI355X over 10-134 MB per tensor: the
+// absmax pass, which ends each block with an atomic, is fastest at
+// QF_ABSMAX_CPT, the quantisation pass at QF_QUANT_CPT; small tensors need
+// the floor to keep the CUs busy).
 #ifndef QF_ABSMAX_CPT
-#define QF_ABSMAX_CPT 64
+#define QF_ABSMAX_CPT 128
 #endif
 #ifndef QF_QUANT_CPT
-#define QF_QUANT_CPT 4
+#define QF_QUANT_CPT 2
+#endif
+#ifndef QF_MIN_BLOCKS
+#define QF_MIN_BLOCKS 256
 #endif
 #ifndef QF_MAX_BLOCKS
 #define QF_MAX_BLOCKS 16384
@@ -427,9 +432,16 @@ static int make_geo(Geo& g, const void* p, const int64_t* n4, const int64_t* s4,
 static unsigned grid_x(const Geo* g, int es, int cpt) {
     int64_t units = 1;
     for (int i = 0; i < 3; ++i) {
-        const int64_t u = g[i].flat ? (g[i].rows * (g[i].L * es / 16) + cpt * kThreads - 1) / (cpt * kThreads)
-                        : g[i].vec ? g[i].rows * ((g[i].L * es / 16 + kSeg - 1) / kSeg)
-                                   : (g[i].n4[0] * g[i].n4[1] * g[i].n4[2] * g[i].n4[3] + kThreads - 1) / kThreads;
+        int64_t u;
+        if (g[i].flat) {
+            const int64_t chunks = g[i].rows * (g[i].L * es / 16);
+            u = (chunks + cpt * kThreads - 1) / (cpt * kThreads);
+            const int64_t floor_u = chunks < QF_MIN_BLOCKS ? chunks : QF_MIN_BLOCKS;
+            u = u > floor_u ? u : floor_u;
+        } else {
+            u = g[i].vec ? g[i].rows * ((g[i].L * es / 16 + kSeg - 1) / kSeg)
+                         : (g[i].n4[0] * g[i].n4[1] * g[i].n4[2] * g[i].n4[3] + kThreads - 1) / kThreads;
+        }
         units = units > u ? units : u;
     }
     const int64_t cap = g[0].flat && g[1].flat && g[2].flat ? QF_MAX_BLOCKS : 2048;
