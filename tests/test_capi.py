@@ -149,3 +149,23 @@ def test_quantiser_entries_check_arguments(lib):
     ost = (ctypes.c_int64 * 12)(*([128, 128, 32, 1] * 3))
     assert lib.qflash_hip_quantize(fake, fake, fake, _lib.F32, geo, None, fake, fake, ost, fake, None) == -1
     assert b"null" in lib.qflash_hip_last_error()
+
+
+def test_bias_entries_check_arguments(lib):
+    fake = ctypes.c_void_p(64)
+    assert lib.qflash_hip_window_bias(None, fake, 4, 3, 49, 0.25, fake, None) == -1
+    assert b"null" in lib.qflash_hip_last_error()
+    assert lib.qflash_hip_window_bias(fake, None, 4, 3, 49, 0.25, fake, None) == -1
+    assert b"nW must be 1" in lib.qflash_hip_last_error()
+    assert lib.qflash_hip_window_bias(fake, fake, 4, 0, 49, 0.25, fake, None) == -1
+    assert b"shape" in lib.qflash_hip_last_error()
+    assert lib.qflash_hip_window_bias(fake, fake, 4, 3, 49, 0.0, fake, None) == -1
+    assert b"sm_scale" in lib.qflash_hip_last_error()
+    assert lib.qflash_hip_window_bias(fake, fake, 1 << 20, 64, 64, 0.25, fake, None) == -1
+    assert b"too large" in lib.qflash_hip_last_error()
+    assert lib.qflash_hip_mask_bias(fake, 0, 0.25, fake, None) == -1
+    assert b"size" in lib.qflash_hip_last_error()
+    assert lib.qflash_hip_mask_bias(fake, 100, float("nan"), fake, None) == -1
+    assert b"sm_scale" in lib.qflash_hip_last_error()
+    assert lib.qflash_hip_mask_bias(None, 100, 0.25, fake, None) == -1
+    assert b"null" in lib.qflash_hip_last_error()
