@@ -705,6 +705,64 @@ __device__ __forceinline__ void lut_pack_vt(uint32_t* pk, i32x4* vf, const uint3
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) vf[i] = i32x4{t[2 * i].x, t[2 * i].y, t[2 * i + 1].x, t[2 * i + 1].y};
 }
+// The first four score registers only (a partial last step of at most 8
+// keys: registers 4-15 hold padded columns alone): pk[0], the V^T fragments.
+template <int D, int LUT>
+__device__ __forceinline__ void lut_pack_vt4(uint32_t* pk, i32x4* vf, const uint32_t* idx, const int8_t* lv,
+                                             const Frag<D>& fr) {
+    static_assert(LUT >= 0 && LUT + kLutMax <= 65536, "table offset must fit the 16-bit LDS immediate");
+    typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+    const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)lv;
+    uint32_t r0 = idx[0], r1 = idx[1], r2 = idx[2], r3 = idx[3];
+    i32x2 t[2 * (D / 32)];
+#define QF_LUT4                                        \
+    "ds_read_u8 %0, %0 offset:%c[lut]\n\t"             \
+    "ds_read_u8 %1, %1 offset:%c[lut]\n\t"             \
+    "ds_read_u8 %2, %2 offset:%c[lut]\n\t"             \
+    "ds_read_u8 %3, %3 offset:%c[lut]\n\t"
+#define QF_PACK4                                       \
+    "s_waitcnt lgkmcnt(0)\n\t"                          \
+    "v_lshl_or_b32 %0, %1, 8, %0\n\t"                   \
+    "v_lshl_or_b32 %2, %3, 8, %2\n\t"                   \
+    "v_lshl_or_b32 %0, %2, 16, %0"
+    if constexpr (D == 32) {
+        asm volatile(QF_LUT4
+                     "ds_read_b64_tr_b8 %[t0], %[b0]\n\t"
+                     "ds_read_b64_tr_b8 %[t1], %[b0] offset:%c[vo]\n\t" QF_PACK4
+                     : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3), [t0] "=&v"(t[0]), [t1] "=&v"(t[1])
+                     : [b0] "v"(base + fr.v[0]), [vo] "i"(16 * D), [lut] "i"(LUT));
+    } else if constexpr (D == 64) {
+        asm volatile(QF_LUT4
+                     "ds_read_b64_tr_b8 %[t0], %[b0]\n\t"
+                     "ds_read_b64_tr_b8 %[t1], %[b0] offset:%c[vo]\n\t"
+                     "ds_read_b64_tr_b8 %[t2], %[b1]\n\t"
+                     "ds_read_b64_tr_b8 %[t3], %[b1] offset:%c[vo]\n\t" QF_PACK4
+                     : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3), [t0] "=&v"(t[0]), [t1] "=&v"(t[1]),
+                       [t2] "=&v"(t[2]), [t3] "=&v"(t[3])
+                     : [b0] "v"(base + fr.v[0]), [b1] "v"(base + fr.v[1]), [vo] "i"(16 * D), [lut] "i"(LUT));
+    } else {
+        asm volatile(QF_LUT4
+                     "ds_read_b64_tr_b8 %[t0], %[b0]\n\t"
+                     "ds_read_b64_tr_b8 %[t1], %[b0] offset:%c[vo]\n\t"
+                     "ds_read_b64_tr_b8 %[t2], %[b1]\n\t"
+                     "ds_read_b64_tr_b8 %[t3], %[b1] offset:%c[vo]\n\t"
+                     "ds_read_b64_tr_b8 %[t4], %[b2]\n\t"
+                     "ds_read_b64_tr_b8 %[t5], %[b2] offset:%c[vo]\n\t"
+                     "ds_read_b64_tr_b8 %[t6], %[b3]\n\t"
+                     "ds_read_b64_tr_b8 %[t7], %[b3] offset:%c[vo]\n\t" QF_PACK4
+                     : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3), [t0] "=&v"(t[0]), [t1] "=&v"(t[1]),
+                       [t2] "=&v"(t[2]), [t3] "=&v"(t[3]), [t4] "=&v"(t[4]), [t5] "=&v"(t[5]), [t6] "=&v"(t[6]),
+                       [t7] "=&v"(t[7])
+                     : [b0] "v"(base + fr.v[0]), [b1] "v"(base + fr.v[1]), [b2] "v"(base + fr.v[2]),
+                       [b3] "v"(base + fr.v[3]), [vo] "i"(16 * D), [lut] "i"(LUT));
+    }
+#undef QF_LUT4
+#undef QF_PACK4
+    pk[0] = r0;
+    pk[1] = pk[2] = pk[3] = 0u;
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) vf[i] = i32x4{t[2 * i].x, t[2 * i].y, t[2 * i + 1].x, t[2 * i + 1].y};
+}
 #undef QF_LUT_LOADS
 #undef QF_LUT_PACK
 #undef QF_LUT_IDX_OPERANDS
@@ -749,16 +807,36 @@ __device__ __forceinline__ void load_bias(int32_t* bias_v, const Args& a, const 
     }
 }
 
+// max / min over the first TV score registers (three-input chains)
+template <int TV>
+__device__ __forceinline__ int32_t max_first(const i32x16& s) {
+    int32_t m = TV == 1 ? s[0] : max(s[0], s[1]);
+#pragma unroll
+    for (int v = 2; v + 1 < TV; v += 2) m = max3(m, s[v], s[v + 1]);
+    if constexpr (TV > 2 && TV % 2) m = max(m, s[TV - 1]);
+    return m;
+}
+template <int TV>
+__device__ __forceinline__ int32_t min_first(const i32x16& s) {
+    int32_t m = TV == 1 ? s[0] : min(s[0], s[1]);
+#pragma unroll
+    for (int v = 2; v + 1 < TV; v += 2) m = min3(m, s[v], s[v + 1]);
+    if constexpr (TV > 2 && TV % 2) m = min(m, s[TV - 1]);
+    return m;
+}
+
 // S^T tile of one step with bias and padding applied (kernel.py:153-156, :250-253);
 // returns the row max over the 32 columns (both lane halves).
 // smin: the minimum over the real columns when MASKED or need_min (else INT32_MAX).
 // Unmasked: every score carries kScoreBias, from an extra MFMA of xb (all
-// bytes -128) with itself.
-template <int D, bool MASKED, bool TAIL>
+// bytes -128) with itself.  TV < 16 (partial steps of at most 8 keys, TV = 4):
+// registers TV..15 hold padded columns only and are set to the padding value.
+template <int D, bool MASKED, bool TAIL, int TV = 16>
 __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& a, const i32x4* qv,
                                           const int8_t* lk, const Frag<D>& fr, const int32_t* bias_v, int kstart,
                                           int lane, bool need_min, i32x4 xb) {
     constexpr int DB = D / 32;
+    constexpr int32_t PAD = kNegInf + (MASKED ? 0 : kScoreBias);
     // K fragments first: the bias MFMA runs while they are in flight
     i32x4 kf[DB];
 #pragma unroll
@@ -773,37 +851,22 @@ __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& 
     const int32_t tcut = a.N - kstart - 4 * (lane >> 5);
     if constexpr (MASKED) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
+        for (int v = 0; v < TV; ++v) {
             s[v] = wadd(s[v], bias_v[v]);
             if (!TAIL || !padded(v, tcut)) smin = min(smin, s[v]);
         }
     } else if (need_min) {
-        // over all 16 raw scores: a padded column's raw score (its K row reads
-        // as 0) is 0, which can only lower the minimum, so a check that passes
-        // with it passes for the real columns
-        smin = min3(s[0], s[1], s[2]);
-        smin = min3(smin, s[3], s[4]);
-        smin = min3(smin, s[5], s[6]);
-        smin = min3(smin, s[7], s[8]);
-        smin = min3(smin, s[9], s[10]);
-        smin = min3(smin, s[11], s[12]);
-        smin = min3(smin, s[13], s[14]);
-        smin = min(smin, s[15]);
+        // over the raw scores: a padded column's raw score (its K row reads as
+        // 0) is the bias alone, which can only lower the minimum, so a check
+        // that passes with it passes for the real columns
+        smin = min_first<TV>(s);
     }
     if constexpr (TAIL) {
 #pragma unroll
         for (int v = 0; v < 16; ++v)
-            if (padded(v, tcut)) s[v] = kNegInf + (MASKED ? 0 : kScoreBias);
+            if (v >= TV || padded(v, tcut)) s[v] = PAD;
     }
-    int32_t mx = max3(s[0], s[1], s[2]);
-    mx = max3(mx, s[3], s[4]);
-    mx = max3(mx, s[5], s[6]);
-    mx = max3(mx, s[7], s[8]);
-    mx = max3(mx, s[9], s[10]);
-    mx = max3(mx, s[11], s[12]);
-    mx = max3(mx, s[13], s[14]);
-    mx = max(mx, s[15]);
-    return half_max(mx);
+    return half_max(max_first<TV>(s));
 }
 
 // One 32-key step (qflash/kernel.py:147-174) for the 32 query rows of a wave.
@@ -811,7 +874,7 @@ __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& 
 // computation of acc (the accumulators keep their registers across steps).
 // Scores, m and m' carry the bias SB (kScoreBias when unmasked): only their
 // differences enter the arithmetic.  LUT: LDS address of the p table.
-template <int D, int LUT, bool MASKED, bool TAIL, bool WIDE, bool DYN, bool FIRST>
+template <int D, int LUT, bool MASKED, bool TAIL, bool WIDE, bool DYN, bool FIRST, int TV = 16>
 __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const i32x4* qv, const int8_t* lk,
                                           const int8_t* lv, const Frag<D>& fr, const BiasRow& brow, int kstart,
                                           int lane, bool wave_fast, int32_t xlim, int lut_mode, i32x4 xb) {
@@ -824,7 +887,8 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     if constexpr (MASKED) load_bias<TAIL>(bias_v, a, brow, kstart, lane);
     i32x16 s;
     int32_t smin;
-    const int32_t mx = scores<D, MASKED, TAIL>(s, smin, a, qv, lk, fr, bias_v, kstart, lane, lut_mode == 2, xb);
+    static_assert(TV == 16 || (TAIL && TV == 4), "TV < 16: partial steps of at most 8 keys");
+    const int32_t mx = scores<D, MASKED, TAIL, TV>(s, smin, a, qv, lk, fr, bias_v, kstart, lane, lut_mode == 2, xb);
     const int32_t m = st.m;
     const int32_t mn = max(m, mx);  // kernel.py:158
     const int32_t dm = wsub(m, mn);
@@ -850,26 +914,29 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
         if constexpr (MASKED) {
             // real columns: s - thr = lut_n - 1 - u >= lut_n - 1 - lut_lim > INT32_MIN, no wrap
 #pragma unroll
-            for (int v = 0; v < 16; ++v) idx[v] = (uint32_t)max(wsub(s[v], thr), 0);
+            for (int v = 0; v < TV; ++v) idx[v] = (uint32_t)max(wsub(s[v], thr), 0);
         } else {
             // scores and thr in [1, 2^31) (lut_mode != 0 only then): unsigned saturation
 #pragma unroll
-            for (int v = 0; v < 16; ++v) idx[v] = __builtin_elementwise_sub_sat((uint32_t)s[v], (uint32_t)thr);
+            for (int v = 0; v < TV; ++v) idx[v] = __builtin_elementwise_sub_sat((uint32_t)s[v], (uint32_t)thr);
         }
         if constexpr (TAIL) {  // padded columns read entry 0 (p = 0); l gets their p below
             const int32_t tcut = a.N - kstart - 4 * g;
 #pragma unroll
-            for (int v = 0; v < 16; ++v)
+            for (int v = 0; v < TV; ++v)
                 if (padded(v, tcut)) idx[v] = 0;
         }
-        lut_pack_vt<D, LUT>(pk, vf, idx, lv, fr);
+        if constexpr (TV == 4)
+            lut_pack_vt4<D, LUT>(pk, vf, idx, lv, fr);
+        else
+            lut_pack_vt<D, LUT>(pk, vf, idx, lv, fr);
     } else if (vec_ok) {
         // kernel.py:159-161 in six ops per score (see the fast-path comment)
         const int32_t c1 = opaque(wadd(wmul(wsub(0, mn), eM), 1 << 16));
         const int32_t c3 = opaque(wsub(rs, mn));
         const int32_t c15 = opaque(1 << 15);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
+        for (int v = 0; v < TV; ++v) {  // registers TV..15 are padded columns (set below)
             const int32_t t = mad24(s[v], eM, c1);
             const int32_t q1 = t >> 16;
             const int32_t av = s[v] + __mul24(q1, rs) + c3;
@@ -1125,6 +1192,9 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
         if (nfull == 0)
             fast_step<D, LUT, MASKED, true, WIDE, DYN, true>(st, a, qv, lk, lv, fr, brow, 0, lane, wave_fast, xlim,
                                                              lut_mode, xb);
+        else if ((a.N & 31) <= 8)  // keys of the first four score registers only
+            fast_step<D, LUT, MASKED, true, WIDE, DYN, false, 4>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane,
+                                                                 wave_fast, xlim, lut_mode, xb);
         else
             fast_step<D, LUT, MASKED, true, WIDE, DYN, false>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane,
                                                               wave_fast, xlim, lut_mode, xb);
