@@ -705,64 +705,91 @@ __device__ __forceinline__ void lut_pack_vt(uint32_t* pk, i32x4* vf, const uint3
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) vf[i] = i32x4{t[2 * i].x, t[2 * i].y, t[2 * i + 1].x, t[2 * i + 1].y};
 }
-// The first four score registers only (a partial last step of at most 8
-// keys: registers 4-15 hold padded columns alone): pk[0], the V^T fragments.
-template <int D, int LUT>
-__device__ __forceinline__ void lut_pack_vt4(uint32_t* pk, i32x4* vf, const uint32_t* idx, const int8_t* lv,
+// The first TV score registers only (TV = 4, 8, 12: a partial last step of at
+// most 2*TV keys, whose registers TV..15 hold padded columns alone): pk[0 ..
+// TV/4 - 1] (the others 0) and the V^T fragments.
+#define QF_L(i) "ds_read_u8 %" #i ", %" #i " offset:%c[lut]\n\t"
+#define QF_P(a, b, c, d)                                      \
+    "v_lshl_or_b32 %" #a ", %" #b ", 8, %" #a "\n\t"            \
+    "v_lshl_or_b32 %" #c ", %" #d ", 8, %" #c "\n\t"            \
+    "v_lshl_or_b32 %" #a ", %" #c ", 16, %" #a "\n\t"
+#define QF_LOADS4 QF_L(0) QF_L(1) QF_L(2) QF_L(3)
+#define QF_LOADS8 QF_LOADS4 QF_L(4) QF_L(5) QF_L(6) QF_L(7)
+#define QF_LOADS12 QF_LOADS8 QF_L(8) QF_L(9) QF_L(10) QF_L(11)
+#define QF_PACK4 "s_waitcnt lgkmcnt(0)\n\t" QF_P(0, 1, 2, 3)
+#define QF_PACK8 QF_PACK4 QF_P(4, 5, 6, 7)
+#define QF_PACK12 QF_PACK8 QF_P(8, 9, 10, 11)
+#define QF_IDX4 "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3])
+#define QF_IDX8 QF_IDX4, "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7])
+#define QF_IDX12 QF_IDX8, "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11])
+#define QF_TR32                                           \
+    "ds_read_b64_tr_b8 %[t0], %[b0]\n\t"                  \
+    "ds_read_b64_tr_b8 %[t1], %[b0] offset:%c[vo]\n\t"
+#define QF_TR64 QF_TR32                                   \
+    "ds_read_b64_tr_b8 %[t2], %[b1]\n\t"                  \
+    "ds_read_b64_tr_b8 %[t3], %[b1] offset:%c[vo]\n\t"
+#define QF_TR128 QF_TR64                                  \
+    "ds_read_b64_tr_b8 %[t4], %[b2]\n\t"                  \
+    "ds_read_b64_tr_b8 %[t5], %[b2] offset:%c[vo]\n\t"    \
+    "ds_read_b64_tr_b8 %[t6], %[b3]\n\t"                  \
+    "ds_read_b64_tr_b8 %[t7], %[b3] offset:%c[vo]\n\t"
+#define QF_T32 [t0] "=&v"(t[0]), [t1] "=&v"(t[1])
+#define QF_T64 QF_T32, [t2] "=&v"(t[2]), [t3] "=&v"(t[3])
+#define QF_T128 QF_T64, [t4] "=&v"(t[4]), [t5] "=&v"(t[5]), [t6] "=&v"(t[6]), [t7] "=&v"(t[7])
+#define QF_B32 [b0] "v"(base + fr.v[0]), [vo] "i"(16 * D), [lut] "i"(LUT)
+#define QF_B64 QF_B32, [b1] "v"(base + fr.v[1])
+#define QF_B128 QF_B64, [b2] "v"(base + fr.v[2]), [b3] "v"(base + fr.v[3])
+#define QF_TV_ASM(LOADS, PACK, IDX)                                                             \
+    if constexpr (D == 32)                                                                      \
+        asm volatile(LOADS QF_TR32 PACK : IDX, QF_T32 : QF_B32);                                \
+    else if constexpr (D == 64)                                                                 \
+        asm volatile(LOADS QF_TR64 PACK : IDX, QF_T64 : QF_B64);                                \
+    else                                                                                        \
+        asm volatile(LOADS QF_TR128 PACK : IDX, QF_T128 : QF_B128);
+template <int D, int LUT, int TV>
+__device__ __forceinline__ void lut_pack_vtn(uint32_t* pk, i32x4* vf, const uint32_t* idx, const int8_t* lv,
                                              const Frag<D>& fr) {
     static_assert(LUT >= 0 && LUT + kLutMax <= 65536, "table offset must fit the 16-bit LDS immediate");
+    static_assert(TV == 4 || TV == 8 || TV == 12, "4, 8 or 12 registers");
     typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
     const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)lv;
-    uint32_t r0 = idx[0], r1 = idx[1], r2 = idx[2], r3 = idx[3];
+    uint32_t r[TV];
+#pragma unroll
+    for (int i = 0; i < TV; ++i) r[i] = idx[i];
     i32x2 t[2 * (D / 32)];
-#define QF_LUT4                                        \
-    "ds_read_u8 %0, %0 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %1, %1 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %2, %2 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %3, %3 offset:%c[lut]\n\t"
-#define QF_PACK4                                       \
-    "s_waitcnt lgkmcnt(0)\n\t"                          \
-    "v_lshl_or_b32 %0, %1, 8, %0\n\t"                   \
-    "v_lshl_or_b32 %2, %3, 8, %2\n\t"                   \
-    "v_lshl_or_b32 %0, %2, 16, %0"
-    if constexpr (D == 32) {
-        asm volatile(QF_LUT4
-                     "ds_read_b64_tr_b8 %[t0], %[b0]\n\t"
-                     "ds_read_b64_tr_b8 %[t1], %[b0] offset:%c[vo]\n\t" QF_PACK4
-                     : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3), [t0] "=&v"(t[0]), [t1] "=&v"(t[1])
-                     : [b0] "v"(base + fr.v[0]), [vo] "i"(16 * D), [lut] "i"(LUT));
-    } else if constexpr (D == 64) {
-        asm volatile(QF_LUT4
-                     "ds_read_b64_tr_b8 %[t0], %[b0]\n\t"
-                     "ds_read_b64_tr_b8 %[t1], %[b0] offset:%c[vo]\n\t"
-                     "ds_read_b64_tr_b8 %[t2], %[b1]\n\t"
-                     "ds_read_b64_tr_b8 %[t3], %[b1] offset:%c[vo]\n\t" QF_PACK4
-                     : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3), [t0] "=&v"(t[0]), [t1] "=&v"(t[1]),
-                       [t2] "=&v"(t[2]), [t3] "=&v"(t[3])
-                     : [b0] "v"(base + fr.v[0]), [b1] "v"(base + fr.v[1]), [vo] "i"(16 * D), [lut] "i"(LUT));
+    if constexpr (TV == 4) {
+        QF_TV_ASM(QF_LOADS4, QF_PACK4, QF_IDX4)
+    } else if constexpr (TV == 8) {
+        QF_TV_ASM(QF_LOADS8, QF_PACK8, QF_IDX8)
     } else {
-        asm volatile(QF_LUT4
-                     "ds_read_b64_tr_b8 %[t0], %[b0]\n\t"
-                     "ds_read_b64_tr_b8 %[t1], %[b0] offset:%c[vo]\n\t"
-                     "ds_read_b64_tr_b8 %[t2], %[b1]\n\t"
-                     "ds_read_b64_tr_b8 %[t3], %[b1] offset:%c[vo]\n\t"
-                     "ds_read_b64_tr_b8 %[t4], %[b2]\n\t"
-                     "ds_read_b64_tr_b8 %[t5], %[b2] offset:%c[vo]\n\t"
-                     "ds_read_b64_tr_b8 %[t6], %[b3]\n\t"
-                     "ds_read_b64_tr_b8 %[t7], %[b3] offset:%c[vo]\n\t" QF_PACK4
-                     : "+v"(r0), "+v"(r1), "+v"(r2), "+v"(r3), [t0] "=&v"(t[0]), [t1] "=&v"(t[1]),
-                       [t2] "=&v"(t[2]), [t3] "=&v"(t[3]), [t4] "=&v"(t[4]), [t5] "=&v"(t[5]), [t6] "=&v"(t[6]),
-                       [t7] "=&v"(t[7])
-                     : [b0] "v"(base + fr.v[0]), [b1] "v"(base + fr.v[1]), [b2] "v"(base + fr.v[2]),
-                       [b3] "v"(base + fr.v[3]), [vo] "i"(16 * D), [lut] "i"(LUT));
+        QF_TV_ASM(QF_LOADS12, QF_PACK12, QF_IDX12)
     }
-#undef QF_LUT4
-#undef QF_PACK4
-    pk[0] = r0;
-    pk[1] = pk[2] = pk[3] = 0u;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) pk[w] = 4 * w < TV ? r[4 * w < TV ? 4 * w : 0] : 0u;
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) vf[i] = i32x4{t[2 * i].x, t[2 * i].y, t[2 * i + 1].x, t[2 * i + 1].y};
 }
+#undef QF_L
+#undef QF_P
+#undef QF_LOADS4
+#undef QF_LOADS8
+#undef QF_LOADS12
+#undef QF_PACK4
+#undef QF_PACK8
+#undef QF_PACK12
+#undef QF_IDX4
+#undef QF_IDX8
+#undef QF_IDX12
+#undef QF_TR32
+#undef QF_TR64
+#undef QF_TR128
+#undef QF_T32
+#undef QF_T64
+#undef QF_T128
+#undef QF_B32
+#undef QF_B64
+#undef QF_B128
+#undef QF_TV_ASM
 #undef QF_LUT_LOADS
 #undef QF_LUT_PACK
 #undef QF_LUT_IDX_OPERANDS
@@ -829,7 +856,7 @@ __device__ __forceinline__ int32_t min_first(const i32x16& s) {
 // returns the row max over the 32 columns (both lane halves).
 // smin: the minimum over the real columns when MASKED or need_min (else INT32_MAX).
 // Unmasked: every score carries kScoreBias, from an extra MFMA of xb (all
-// bytes -128) with itself.  TV < 16 (partial steps of at most 8 keys, TV = 4):
+// bytes -128) with itself.  TV < 16 (partial steps of at most 2*TV keys):
 // registers TV..15 hold padded columns only and are set to the padding value.
 template <int D, bool MASKED, bool TAIL, int TV = 16>
 __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& a, const i32x4* qv,
@@ -887,7 +914,7 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     if constexpr (MASKED) load_bias<TAIL>(bias_v, a, brow, kstart, lane);
     i32x16 s;
     int32_t smin;
-    static_assert(TV == 16 || (TAIL && TV == 4), "TV < 16: partial steps of at most 8 keys");
+    static_assert(TV == 16 || (TAIL && (TV == 4 || TV == 8 || TV == 12)), "TV < 16: partial steps of <= 2*TV keys");
     const int32_t mx = scores<D, MASKED, TAIL, TV>(s, smin, a, qv, lk, fr, bias_v, kstart, lane, lut_mode == 2, xb);
     const int32_t m = st.m;
     const int32_t mn = max(m, mx);  // kernel.py:158
@@ -926,8 +953,8 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
             for (int v = 0; v < TV; ++v)
                 if (padded(v, tcut)) idx[v] = 0;
         }
-        if constexpr (TV == 4)
-            lut_pack_vt4<D, LUT>(pk, vf, idx, lv, fr);
+        if constexpr (TV < 16)
+            lut_pack_vtn<D, LUT, TV>(pk, vf, idx, lv, fr);
         else
             lut_pack_vt<D, LUT>(pk, vf, idx, lv, fr);
     } else if (vec_ok) {
@@ -1192,9 +1219,15 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
         if (nfull == 0)
             fast_step<D, LUT, MASKED, true, WIDE, DYN, true>(st, a, qv, lk, lv, fr, brow, 0, lane, wave_fast, xlim,
                                                              lut_mode, xb);
-        else if ((a.N & 31) <= 8)  // keys of the first four score registers only
+        else if ((a.N & 31) <= 8)  // keys of the first TV score registers only
             fast_step<D, LUT, MASKED, true, WIDE, DYN, false, 4>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane,
                                                                  wave_fast, xlim, lut_mode, xb);
+        else if ((a.N & 31) <= 16)
+            fast_step<D, LUT, MASKED, true, WIDE, DYN, false, 8>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane,
+                                                                 wave_fast, xlim, lut_mode, xb);
+        else if ((a.N & 31) <= 24)
+            fast_step<D, LUT, MASKED, true, WIDE, DYN, false, 12>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane,
+                                                                  wave_fast, xlim, lut_mode, xb);
         else
             fast_step<D, LUT, MASKED, true, WIDE, DYN, false>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane,
                                                               wave_fast, xlim, lut_mode, xb);
