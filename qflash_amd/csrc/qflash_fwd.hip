@@ -1168,12 +1168,12 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
 #pragma unroll
     for (int t = 0; t < DB; ++t) st.acc[t] = i32x16{};
     st.m = kNegInf + (MASKED ? 0 : kScoreBias);  // kernel.py:138
+    st.l = 1;                                     // kernel.py:139
+    st.bnd = 0.f;
+    st.wide = 0;
     // all bytes -128; opaque to the compiler each step, so that the bias MFMA
     // is issued per step rather than hoisted into 16 live registers
     i32x4 xb = i32x4{(int32_t)0x80808080, (int32_t)0x80808080, (int32_t)0x80808080, (int32_t)0x80808080};
-    st.l = 1;        // kernel.py:139
-    st.bnd = 0.f;
-    st.wide = 0;
 
     // K / V of this head as buffers ending after row N-1: rows >= N read as 0
     const __amdgpu_buffer_rsrc_t rk =
