@@ -271,12 +271,13 @@ def test_table_path_at_score_bias_edge(sm_scale, monkeypatch):
 
 @pytest.mark.parametrize("masked", [False, True])
 @pytest.mark.parametrize("D", [32, 64])
-@pytest.mark.parametrize("N", [33, 36, 37, 49, 68])
+@pytest.mark.parametrize("N", [33, 36, 37, 40, 41, 48, 49, 56, 57, 68])
 def test_table_path_short_tails(N, D, masked, monkeypatch):
     """Partial last steps of 1-5 keys (the upper lane half of the step has no
-    real column up to 4) and 17 keys, on the table path, masked or not: the
-    padded columns read entry 0 and l gets their exact p; small score spreads
-    and a small bias keep every step on the table."""
+    real column up to 4), 8/9, 16/17 and 24/25 keys (the edges of the kernel's
+    4-, 8-, 12- and 16-register last steps), on the table path, masked or
+    not: the padded columns read entry 0 and l gets their exact p; small
+    score spreads and a small bias keep every step on the table."""
     monkeypatch.setenv("QFLASH_HIP_FORCE_LUT", "1")
     from qflash_amd.kernel import fixed_point_constants
     consts = Consts(*fixed_point_constants(1 / 57.3, 30, 30))
