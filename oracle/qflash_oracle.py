@@ -25,10 +25,16 @@ Pinning status per function (what fails if the restatement is wrong):
   vectors from the reference kernel run under the Triton interpreter, plus
   closed-form properties (E(0)=rs, E(-rs*k) ~= rs>>k, monotone segments).
 * the kernel loop (K0-K6): golden vectors (masked/unmasked, N%32 != 0,
-  fp16/fp32 hosts), scalar/numpy/C agreement, BLOCK_M independence and an
-  SQNR floor against fp32 softmax attention.
-* host constants and quantiser: golden vectors of the reference host path
-  (``qflash_forward``) for fp32 and fp16 inputs.
+  fp16/fp32 hosts), scalar/numpy/C agreement, planted mistakes, and an SQNR
+  floor against fp32 softmax attention on uniform inputs
+  (tests/test_oracle_golden.py, tests/test_oracle_host.py).
+* host_constants, quantize_ref_torch, mask_to_bias_torch: the constants,
+  int8 codes and int32 biases of the reference host path's launch records
+  for fp32 and fp16 inputs, half-to-even ties, the raising cases, planted
+  mistakes (tests/test_oracle_host.py).
+* sqnr_db: hand-computed norms; softmax_attention_fp32: closed forms (equal
+  logits -> mean of V, a dominant logit -> its V row, -inf bias); both with
+  planted mistakes (tests/test_oracle_host.py).
 """
 from __future__ import annotations
 
