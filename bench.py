@@ -12,8 +12,15 @@ resident in HBM.  Prints ONE JSON line:
   sqnr_db    dequantised output vs fp32 softmax attention of the
              unquantised inputs
 
+  per_config cfg1..cfg5 (cfg4 also with the reference's materialised bias)
+             x seeds 0, 1, 2: us/call, flushed us/call, TOPS, fractions of
+             the MFMA peak and of the roofline, SQNR, end-to-end us
+
+Timing: `--settle-ms` of back-to-back launches first (the clocks reach their
+loaded state), then W warmup launches, then K timed ones.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3]
-       [--all-configs] [--no-cpu]
+       [--settle-ms MS] [--no-per-config] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -95,6 +102,24 @@ def make_step(w):
         def step():
             qflash_masked_kernel[None](q8, k8, v8, o, bias, *c, *st, *bst, cfg.Z, cfg.H, **kw)
     return step
+
+
+def settle(step, ms: float) -> dict:
+    """Launch `step` back to back for about `ms` milliseconds of wall time, so
+    that the GPU's clocks reach their loaded state before anything is timed
+    (the reference warms up for a fixed 10 ms, kernel.py:349).  Returns the
+    time spent and the launches made."""
+    import torch
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n = 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(8):
+            step()
+        n += 8
+        torch.cuda.synchronize()
+    return {"settle_ms": (time.perf_counter() - t0) * 1e3, "settle_launches": n}
 
 
 def time_steps(step, steps: int, warmup: int):
@@ -193,28 +218,64 @@ def cpu_baseline(w, threads: int):
             "us_per_call_equiv": dt * 1e6 * zh / n, "codes_match_gpu": same}
 
 
+def roofline_us(cfg) -> float:
+    """The call's lower bound on MI355X: max(ops / int8 MFMA peak, bytes / HBM peak), in us."""
+    return max(cfg.ops / (PEAK_INT8_TOPS * 1e12), cfg.bytes_min / (PEAK_HBM_GBS * 1e9)) * 1e6
+
+
 def run_config(name: str, steps: int, warmup: int, dev, seed: int = 0, cpu: bool = False,
-               dense_bias: bool = False, time_ms=None):
-    """One configuration: `steps` timed launches after `warmup` ones, or, with
-    time_ms = (warmup ms, timed ms), counts derived from a 3-launch estimate."""
+               dense_bias: bool = False, time_ms=None, settle_ms: float = 0.0, e2e: bool = True):
+    """One configuration: `settle_ms` of back-to-back launches, then `steps`
+    timed launches after `warmup` ones, or, with time_ms = (warmup ms, timed
+    ms), counts derived from a 3-launch estimate."""
     w = prepare(name, seed, dev, dense_bias=dense_bias)
     step = make_step(w)
+    st = settle(step, settle_ms) if settle_ms > 0 else {"settle_ms": 0.0, "settle_launches": 0}
     if time_ms is not None:
         _, est_ms, _ = time_steps(step, 3, 1)
         warmup = int(min(400, max(5, time_ms[0] / est_ms)))
         steps = int(min(1000, max(10, time_ms[1] / est_ms)))
     wall_ms, ev_mean_ms, ev_med_ms = time_steps(step, steps, warmup)
     cfg = w["cfg"]
-    res = {"config": name + ("-dense-bias" if dense_bias else ""), "workload": cfg.name, "ops": cfg.ops,
-           "ms_per_step": wall_ms,
+    res = {"config": name + ("-dense-bias" if dense_bias else ""), "seed": seed, "workload": cfg.name,
+           "ops": cfg.ops, "ms_per_step": wall_ms, "steps": steps, "warmup": warmup, **st,
            "us_per_call": ev_mean_ms * 1e3, "us_per_call_median": ev_med_ms * 1e3,
            "us_per_call_flushed": flushed_us(step), "tops": cfg.ops / (wall_ms * 1e-3) / 1e12,
            "kernel_tops": cfg.ops / (ev_mean_ms * 1e-3) / 1e12, "sqnr_db": sqnr_db(w, dev),
            "hbm_gbs_algorithmic": cfg.bytes_min / (ev_mean_ms * 1e-3) / 1e9}
-    res["e2e_us"] = e2e_us(w, dev)
+    res["mfma_frac"] = res["kernel_tops"] / PEAK_INT8_TOPS
+    res["roofline_us"] = roofline_us(cfg)
+    res["roofline_frac"] = res["roofline_us"] / (ev_mean_ms * 1e3)
+    if e2e:
+        res["e2e_us"] = e2e_us(w, dev)
     if cpu:
         res["cpu_baseline"] = cpu_baseline(w, host_cores())
     return res
+
+
+PER_CONFIG_KEYS = ("config", "seed", "us_per_call", "us_per_call_median", "us_per_call_flushed", "kernel_tops",
+                   "mfma_frac", "roofline_us", "roofline_frac", "sqnr_db", "hbm_gbs_algorithmic", "e2e_us")
+
+
+def per_config(dev, head=None, seeds=(0, 1, 2)):
+    """cfg1..cfg5 (and cfg4 with the reference's materialised bias) for each seed:
+    us/call after a clock-settle phase, flushed us/call, TOPS, fractions of the
+    MFMA peak and of the roofline, SQNR, end-to-end us (seed 0 only)."""
+    from qflash_amd.workloads import CONFIGS
+
+    out = []
+    for name in CONFIGS:
+        for dense in ((False, True) if CONFIGS[name].swin else (False,)):
+            for seed in seeds:
+                if head is not None and not dense and name == head["config"] and seed == head["seed"]:
+                    r = head
+                else:
+                    r = run_config(name, 0, 0, dev, seed, dense_bias=dense, time_ms=(10.0, 60.0),
+                                   settle_ms=60.0, e2e=seed == seeds[0])
+                out.append({k: r[k] for k in PER_CONFIG_KEYS if k in r})
+                print(f"bench.py: {out[-1]['config']} seed {seed}: {out[-1]['us_per_call']:.1f} us/call, "
+                      f"SQNR {out[-1]['sqnr_db']:.2f} dB", file=sys.stderr, flush=True)
+    return out
 
 
 def e2e_call(w, dev):
@@ -264,12 +325,16 @@ def e2e_us(w, dev, reps: int = 10) -> float:
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # defaults: ~40 ms of warmup (the clocks settle) and ~50 ms of timed launches at cfg3
+    # defaults: ~50 ms of timed launches at cfg3 after the settle phase and 20 warmup launches
     ap.add_argument("--steps", type=int, default=400)
-    ap.add_argument("--warmup", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="cfg3")
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--all-configs", action="store_true", help="also time cfg1..cfg5 (per_config field)")
+    ap.add_argument("--settle-ms", type=float, default=300.0,
+                    help="wall time of back-to-back launches before the warmup steps (clocks settle)")
+    ap.add_argument("--no-per-config", action="store_true",
+                    help="skip the per_config block (cfg1..cfg5 x seeds 0, 1, 2)")
+    ap.add_argument("--all-configs", action="store_true", help=argparse.SUPPRESS)  # per_config is the default
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--profile", action="store_true",
                     help="only the timed kernel launches (for rocprofv3 counter runs)")
@@ -323,10 +388,14 @@ def main(argv=None):
             workloads.CONFIGS["shape"] = workloads.Config(f"Z{Z} H{H} N{N} D{D}", Z, H, N, D)
             args.config = "shape"
         w = prepare(args.config, args.seed, dev)
-        wall, ev, _ = time_steps(make_step(w), args.steps, args.warmup)
+        step = make_step(w)
+        if args.settle_ms > 0:
+            settle(step, args.settle_ms)
+        wall, ev, _ = time_steps(step, args.steps, args.warmup)
         print(json.dumps({"config": args.config, "steps": args.steps, "us_per_call": ev * 1e3}), flush=True)
         return 0
-    head = run_config(args.config, args.steps, args.warmup, dev, args.seed, cpu=not args.no_cpu)
+    head = run_config(args.config, args.steps, args.warmup, dev, args.seed, cpu=not args.no_cpu,
+                      settle_ms=args.settle_ms)
     cfg_ops = head["ops"]
     traffic = read_traffic() if args.config == "cfg3" else None
     achieved = head["kernel_tops"]
@@ -346,32 +415,27 @@ def main(argv=None):
         "config": {"workload": head["workload"], "Z": None, "H": None, "N": None, "D": None,
                    "seed": args.seed, "layout": "token-major (B,N,H,D) int8, as QAttention produces",
                    "timed": "kernel only, int8 Q/K/V resident in HBM"},
+        "settle_ms": head["settle_ms"],
+        "settle_launches": head["settle_launches"],
         "us_per_call": head["us_per_call"],
+        "us_per_call_median": head["us_per_call_median"],
         "us_per_call_flushed": head["us_per_call_flushed"],
         "e2e_us": head["e2e_us"],
         "sqnr_db": head["sqnr_db"],
-        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_INT8_TOPS, "unit": "TOPS",
                      "frac": achieved / PEAK_INT8_TOPS, "traffic": traffic,
-                     "note": "int8 tera-ops/s (2 ops per MAC, 4*Z*H*N^2*D per call) vs 5.0 POPS dense int8",
+                     "note": "int8 tera-operations/s (2 ops per MAC, 4*Z*H*N^2*D per call, HIP events on the "
+                             "launch stream) vs 5.0 POPS dense int8 MFMA",
                      "ops_per_launch": cfg_ops,
+                     "roofline_us": head["roofline_us"], "roofline_frac": head["roofline_frac"],
                      "hbm_gbs_algorithmic": head["hbm_gbs_algorithmic"]},
         "cpu_baseline": head.get("cpu_baseline"),
     }
     from qflash_amd.workloads import CONFIGS
     c = CONFIGS[args.config]
     line["config"].update(Z=c.Z, H=c.H, N=c.N, D=c.D)
-    if args.all_configs:
-        per = []
-        for name in CONFIGS:
-            # about 50 ms of warmup (the clocks settle) and 100 ms of timed launches per configuration
-            r = head if name == args.config else run_config(name, 0, 0, dev, args.seed, time_ms=(50.0, 100.0))
-            per.append({k: r[k] for k in ("config", "us_per_call", "us_per_call_flushed", "kernel_tops",
-                                          "sqnr_db", "hbm_gbs_algorithmic", "e2e_us")})
-            if CONFIGS[name].swin:  # the reference's materialised (Z, H, N, N) bias, for comparison
-                r = run_config(name, 0, 0, dev, args.seed, dense_bias=True, time_ms=(50.0, 100.0))
-                per.append({k: r[k] for k in ("config", "us_per_call", "us_per_call_flushed", "kernel_tops",
-                                              "sqnr_db", "hbm_gbs_algorithmic", "e2e_us")})
-        line["per_config"] = per
+    if not args.no_per_config:
+        line["per_config"] = per_config(dev, head)
     print(json.dumps(line), flush=True)
     return 0
 

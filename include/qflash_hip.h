@@ -19,7 +19,8 @@
  *     default stream); the call returns 0 or a negative QFLASH_HIP_E* code
  *     and never throws; qflash_hip_last_error() gives a message for the
  *     last failure on the calling thread;
- *   - reentrant: no mutable global state besides the per-thread message.
+ *   - reentrant: no mutable global state besides the per-thread message and
+ *     the test-hook bits of qflash_hip_set_test_hooks.
  */
 #ifndef QFLASH_HIP_H
 #define QFLASH_HIP_H
@@ -170,7 +171,6 @@ const char* qflash_hip_last_error(void);
  */
 int qflash_hip_mfma_layout_check(const int8_t* A, const int8_t* B, int32_t* C, void* stream);
 
-/* Library version string (no counterpart in the reference). */
 /*
  * Diagnostic, no counterpart in the reference: the bounds of the table that
  * the fast kernel may use for exp2 + requantisation under these constants
@@ -183,6 +183,24 @@ int qflash_hip_mfma_layout_check(const int8_t* A, const int8_t* B, int32_t* C, v
  */
 int qflash_hip_lut_bounds(int32_t sm_rscale, int32_t exp_M, int32_t req_M, int32_t* lut_n, int32_t* lut_lim);
 
+/*
+ * Test hooks, no counterpart in the reference: each bit forces one of the
+ * exact fallbacks of the attention entry points on inputs that would not need
+ * it, so that tests can drive every path (the codes never change).  The
+ * initial bits come from the environment when the library is loaded
+ * (QFLASH_HIP_FORCE_GENERAL, _FORCE_DYNAMIC_BOUND, _FORCE_ROBUST, _NO_LUT,
+ * _FORCE_LUT = non-zero); no entry point reads the environment afterwards.
+ * Sets the bits for every thread of the process and returns the previous ones.
+ */
+#define QFLASH_HIP_HOOK_FORCE_GENERAL 1u        /* the general kernel */
+#define QFLASH_HIP_HOOK_FORCE_DYNAMIC_BOUND 2u  /* the fast kernel's per-row rescale bound */
+#define QFLASH_HIP_HOOK_FORCE_ROBUST 4u         /* the fast kernel's general arithmetic */
+#define QFLASH_HIP_HOOK_NO_LUT 8u               /* no exp2 table */
+#define QFLASH_HIP_HOOK_FORCE_LUT 16u           /* the exp2 table whatever the launch size */
+#define QFLASH_HIP_HOOK_ALL 31u
+uint32_t qflash_hip_set_test_hooks(uint32_t bits);
+
+/* Library version string (no counterpart in the reference). */
 const char* qflash_hip_version(void);
 
 #ifdef __cplusplus

@@ -34,7 +34,11 @@ EXPORTS = ("qflash_hip_kernel", "qflash_hip_masked_kernel", "qflash_hip_window_k
            "qflash_hip_scales",
            "qflash_hip_quantize", "qflash_hip_window_bias", "qflash_hip_mask_bias",
            "qflash_hip_last_error",
-           "qflash_hip_mfma_layout_check", "qflash_hip_lut_bounds", "qflash_hip_version")
+           "qflash_hip_mfma_layout_check", "qflash_hip_lut_bounds", "qflash_hip_set_test_hooks",
+           "qflash_hip_version")
+
+# test-hook bits of qflash_hip_set_test_hooks (include/qflash_hip.h)
+HOOKS = {"FORCE_GENERAL": 1, "FORCE_DYNAMIC_BOUND": 2, "FORCE_ROBUST": 4, "NO_LUT": 8, "FORCE_LUT": 16}
 
 # element type codes of qflash_hip_scales / qflash_hip_quantize, and its workspace
 F32, F16, BF16, I8 = 0, 1, 2, 3
@@ -74,6 +78,8 @@ def _declare(L):
     L.qflash_hip_mfma_layout_check.argtypes = [vp, vp, vp, vp]
     L.qflash_hip_lut_bounds.restype = ctypes.c_int
     L.qflash_hip_lut_bounds.argtypes = [i32, i32, i32, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]
+    L.qflash_hip_set_test_hooks.restype = ctypes.c_uint32
+    L.qflash_hip_set_test_hooks.argtypes = [ctypes.c_uint32]
     L.qflash_hip_version.restype = ctypes.c_char_p
     L.qflash_hip_version.argtypes = []
 
@@ -105,3 +111,12 @@ def check(rc: int, what: str) -> None:
         msg = load().qflash_hip_last_error().decode(errors="replace")
         cls = QFlashCompilationError if rc == E_HEADDIM else QFlashLibraryError
         raise cls(f"{what} failed ({rc}): {msg}")
+
+
+def set_test_hooks(*names: str) -> int:
+    """Set the library's test hooks to exactly `names` (keys of HOOKS); returns
+    the previous bits.  Tests only: each hook forces an exact fallback path."""
+    bits = 0
+    for n in names:
+        bits |= HOOKS[n]
+    return int(load().qflash_hip_set_test_hooks(bits))

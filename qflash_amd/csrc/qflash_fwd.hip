@@ -21,1322 +21,9 @@
 //   C (32 x 32 int32): lane l, register v holds (row 8*(v/4)+4*(l/32)+v%4,
 //                      col l%32)
 //   (checked at run time by qflash_hip_mfma_layout_check).
-#include <hip/hip_runtime.h>
-#include <hip/hip_fp16.h>
-#include <atomic>
-#include <utility>
-#include <stdint.h>
-#include <stdarg.h>
-#include <stdio.h>
-#include <stdlib.h>
-#include <string.h>
-
-#include "../../include/qflash_hip.h"
-#include "qf_common.h"
+#include "qf_fwd.h"
 
 namespace qf {
-
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
-
-constexpr int32_t kNegInf = -(1 << 20);  // kernel.py:137
-#ifndef QF_FAST_WAVES_D64
-#define QF_FAST_WAVES_D64 4
-#endif
-constexpr int kBN = 32;                   // kernel.py:27, one rescale step
-constexpr int kLutMax = 4096;             // bytes of LDS for the p(u) table of the fast kernel
-// The unmasked fast kernel carries every score (and the running max) plus
-// kScoreBias: one extra MFMA of two all-(-128) operands starts each score tile
-// at 32 * 128 * 128.  Every difference the algorithm takes is unchanged, and a
-// wave whose scores stay above -kScoreBias + kLutMax (128 * ||q_row||_1 below
-// that) has all scores and table thresholds positive, so one saturating
-// subtraction per score gives its table index.
-constexpr int32_t kScoreBias = 32 * 128 * 128;
-
-struct Args {
-    const int8_t* q;
-    const int8_t* k;
-    const int8_t* v;
-    int8_t* o;
-    const int32_t* bias;
-    int64_t sq[4], sk[4], sv[4], so[4], sb[4];
-    int32_t Z, H, N;
-    int32_t rs, eM, rM, lM, aM;
-    int32_t l_shift, acc_shift;
-    int32_t exp_mode, l_mode, acc_mode;  // 1 = shift variant, 0 = idiv
-    int32_t mblocks;                     // workgroups per (z, h)
-    // fast path (set by the host after proving its guards, see choose_path)
-    int32_t id_ok;   // acc rescale by alpha == sm_rscale is the identity (bound on |acc|)
-    int32_t x_safe;  // masked: largest |s - m'| the 24-bit exp path accepts
-    int32_t eps_abs; // | |eM|*rs - 2^16 |
-    int32_t e_acc;   // | rs*acc_M - 2^acc_shift |
-    int32_t force_robust;  // test hook: general arithmetic for every score, alpha and l
-    int32_t n_wg;    // workgroups in the grid (XCD-aware order)
-    int32_t bias_zmod;  // > 0: the bias of batch index z is bias[z % bias_zmod] (window-periodic)
-    int32_t bias_vec;   // bias rows have unit key stride and non-negative strides: 16-byte buffer loads
-    // exp2 + requantisation by table (see lut_pack_vt): p(u) = p(min(u, lut_n - 1))
-    // for u = m' - s in [0, lut_lim], the table holding p(0 .. lut_n - 1) in reverse
-    int32_t lut_n;      // table entries (the last one 0), 0 = no table
-    int32_t lut_lim;
-    // output: int8 codes at `o` (out_dt == QFLASH_HIP_I8), or RN_T(code * o_scale)
-    // of type out_dt at the same element offsets of `out_t` (qflash/kernel.py:351)
-    void* out_t;
-    int32_t out_dt;
-    const void* o_scale;
-};
-
-__device__ __forceinline__ int out_esize(int dt) { return dt == QFLASH_HIP_I8 ? 1 : (dt == QFLASH_HIP_F32 ? 4 : 2); }
-
-// o * o_scale in torch's arithmetic: the int8 code and the scale as fp32, one
-// rounding to the output type.
-__device__ __forceinline__ float scale_value(const Args& a) {
-    if (a.out_dt == QFLASH_HIP_F32) return *reinterpret_cast<const float*>(a.o_scale);
-    const uint32_t h = *reinterpret_cast<const uint16_t*>(a.o_scale);
-    return a.out_dt == QFLASH_HIP_F16 ? __half2float(__ushort_as_half((unsigned short)h)) : __uint_as_float(h << 16);
-}
-
-// Stores the output element of `code` at element offset voff + soff of the
-// head's output buffer (rsrc covers the head; offsets in elements).
-template <int OUT>
-__device__ __forceinline__ void put_out(__amdgpu_buffer_rsrc_t rsrc, int32_t code, int32_t voff, int32_t soff,
-                                        float os) {
-    if constexpr (OUT == QFLASH_HIP_I8) {
-        __builtin_amdgcn_raw_buffer_store_b8((uint8_t)code, rsrc, voff, soff, 0);
-    } else if constexpr (OUT == QFLASH_HIP_F32) {
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint((float)(int8_t)code * os), rsrc, 4 * voff, 4 * soff, 0);
-    } else if constexpr (OUT == QFLASH_HIP_F16) {
-        __builtin_amdgcn_raw_buffer_store_b16(__half_as_ushort(__float2half_rn((float)(int8_t)code * os)), rsrc,
-                                              2 * voff, 2 * soff, 0);
-    } else {
-        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)qf_bf16_bits((float)(int8_t)code * os), rsrc, 2 * voff,
-                                              2 * soff, 0);
-    }
-}
-
-// Calls f.template operator()<OUT>() for the output type of the launch (one
-// uniform branch per wave instead of one per stored element).
-template <typename F>
-__device__ __forceinline__ void with_out_type(int dt, F&& f) {
-    switch (dt) {
-        case QFLASH_HIP_I8: f.template operator()<QFLASH_HIP_I8>(); break;
-        case QFLASH_HIP_F32: f.template operator()<QFLASH_HIP_F32>(); break;
-        case QFLASH_HIP_F16: f.template operator()<QFLASH_HIP_F16>(); break;
-        default: f.template operator()<QFLASH_HIP_BF16>();
-    }
-}
-
-// Buffer over one head's output, ending after row N-1 (element strides so).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t out_rsrc(const Args& a, int z, int h, int D) {
-    const int es = out_esize(a.out_dt);
-    void* base = a.out_dt == QFLASH_HIP_I8 ? (void*)(a.o + z * a.so[0] + h * a.so[1])
-                                           : (void*)((char*)a.out_t + (z * a.so[0] + h * a.so[1]) * es);
-    return __builtin_amdgcn_make_buffer_rsrc(base, 0, ((a.N - 1) * (int32_t)a.so[2] + (D - 1) * (int32_t)a.so[3] + 1) * es,
-                                             0x00020000);
-}
-
-// ----------------------------------------------------------------------------
-// Integer primitives with the reference's (Triton) semantics: int32 wraps,
-// `>>` by a count >= 32 (read as unsigned) gives the sign fill, `//`
-// truncates.  AMD's 32-bit shifts use only the low 5 bits of the count, so
-// the clamp is explicit.
-__host__ __device__ __forceinline__ int32_t wadd(int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); }
-__host__ __device__ __forceinline__ int32_t wsub(int32_t a, int32_t b) { return (int32_t)((uint32_t)a - (uint32_t)b); }
-__host__ __device__ __forceinline__ int32_t wmul(int32_t a, int32_t b) { return (int32_t)((uint32_t)a * (uint32_t)b); }
-__host__ __device__ __forceinline__ int32_t sra(int32_t a, int32_t b) {
-    return (uint32_t)b > 31u ? (a >> 31) : (a >> b);
-}
-
-// exp2_i32: kernel.py:40-59.
-__host__ __device__ __forceinline__ int32_t exp2_i32(int32_t x, const Args& a) {
-    int32_t q = a.exp_mode ? (wmul(x, a.eM) >> 16) : (wsub(0, x) / a.rs);
-    int32_t r = wadd(x, wmul(q, a.rs));
-    return sra(wadd(r >> 1, a.rs), q);
-}
-
-// requantize: kernel.py:62-64 (int8 wrap of the rounded product).
-__host__ __device__ __forceinline__ int32_t requant(int32_t e, const Args& a) {
-    return (int32_t)(int8_t)(wadd(wmul(e, a.rM), 1 << 15) >> 16);
-}
-
-// scale_release: kernel.py:67-82.
-__device__ __forceinline__ int32_t release(int32_t x, int32_t alpha, int32_t M, int32_t shift, int32_t mode,
-                                           int32_t rs) {
-    if (mode) {
-        uint64_t prod = (uint64_t)((int64_t)x * (int64_t)alpha) * (uint64_t)(int64_t)M;
-        prod += 1ull << (shift - 1);
-        return (int32_t)(uint32_t)(uint64_t)((int64_t)prod >> shift);
-    }
-    return wmul(x, alpha) / rs;
-}
-
-// fp32 -> int32 as the reference's CPU path does it: truncate, INT_MIN for
-// NaN / inf / out of range (v_cvt_i32_f32 would saturate instead).
-__device__ __forceinline__ int32_t cvt_x86(float f) {
-    return (f >= -2147483648.0f && f < 2147483648.0f) ? (int32_t)f : (int32_t)0x80000000;
-}
-
-__device__ __forceinline__ i32x16 mfma32(i32x4 a, i32x4 b, i32x16 c) {
-    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
-}
-
-// Row (within a 32-row block) held by result register v of lane l.
-__device__ __forceinline__ int crow(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
-// Key column kstart + crow(v, lane) lies past N (a padded column of the last
-// step) iff 8*(v>>2) + (v&3) >= tcut, tcut = N - kstart - 4*(lane>>5): one
-// per-lane value and compile-time constants, instead of 16 column indices.
-__device__ __forceinline__ bool padded(int v, int32_t tcut) { return 8 * (v >> 2) + (v & 3) >= tcut; }
-
-// 16 bytes from global memory; `vec` = base 16-byte aligned and unit stride.
-template <bool VEC>
-__device__ __forceinline__ i32x4 load16(const int8_t* p, int64_t sd, bool valid) {
-    i32x4 r = {0, 0, 0, 0};
-    if (!valid) return r;
-    if constexpr (VEC) {
-        r = *reinterpret_cast<const i32x4*>(p);
-    } else {
-        uint32_t w[4] = {0, 0, 0, 0};
-        for (int b = 0; b < 16; ++b) w[b >> 2] |= (uint32_t)(uint8_t)p[b * sd] << (8 * (b & 3));
-        r = i32x4{(int32_t)w[0], (int32_t)w[1], (int32_t)w[2], (int32_t)w[3]};
-    }
-    return r;
-}
-
-template <bool VEC>
-__device__ __forceinline__ uint32_t load4(const int8_t* p, int64_t sd, bool valid) {
-    if (!valid) return 0;
-    if constexpr (VEC) {
-        return *reinterpret_cast<const uint32_t*>(p);
-    } else {
-        uint32_t w = 0;
-        for (int b = 0; b < 4; ++b) w |= (uint32_t)(uint8_t)p[b * sd] << (8 * b);
-        return w;
-    }
-}
-
-// LDS tile geometry.  K: 32 rows of D bytes (+16 pad).  V^T: D rows of 32
-// bytes (+16 pad); within a row, byte 16*g + b holds key 8*(b/4)+4*g+b%4,
-// the key that S^T's result register b of lane-half g refers to.
-template <int D>
-struct Tile {
-    static constexpr int RK = D + 16;
-    static constexpr int RV = 48;
-    static constexpr int KBYTES = 32 * RK;
-    static constexpr int VBYTES = D * RV;
-    static constexpr int BYTES = KBYTES + VBYTES;
-};
-
-// Stage keys [kstart, kstart+32) of K and V into LDS (zero past N).
-template <int D, int NT, bool VEC>
-__device__ __forceinline__ void stage_kv(const Args& a, const int8_t* kb, const int8_t* vb, int kstart,
-                                         int8_t* lk, int8_t* lvt, int tid) {
-    using T = Tile<D>;
-    constexpr int KCH = 32 * (D / 16);
-    for (int idx = tid; idx < KCH; idx += NT) {
-        int r = idx / (D / 16), c = idx % (D / 16);
-        int j = kstart + r;
-        i32x4 x = load16<VEC>(kb + (int64_t)j * a.sk[2] + (int64_t)c * 16 * a.sk[3], a.sk[3], j < a.N);
-        *reinterpret_cast<i32x4*>(lk + r * T::RK + c * 16) = x;
-    }
-    constexpr int VBL = 8 * (D / 4);
-    for (int idx = tid; idx < VBL; idx += NT) {
-        int kg = idx / (D / 4), dg = idx % (D / 4);
-        uint32_t r4[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            int j = kstart + 4 * kg + i;
-            r4[i] = load4<VEC>(vb + (int64_t)j * a.sv[2] + (int64_t)dg * 4 * a.sv[3], a.sv[3], j < a.N);
-        }
-        int off = (kg & 1) * 16 + (kg >> 1) * 4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            uint32_t c = ((r4[0] >> (8 * i)) & 0xffu) | (((r4[1] >> (8 * i)) & 0xffu) << 8) |
-                         (((r4[2] >> (8 * i)) & 0xffu) << 16) | (((r4[3] >> (8 * i)) & 0xffu) << 24);
-            *reinterpret_cast<uint32_t*>(lvt + (dg * 4 + i) * T::RV + off) = c;
-        }
-    }
-}
-
-// The reference algorithm with general (wrapping, clamping, 64-bit) integer
-// arithmetic on every element: exact for any constants and inputs.
-template <int D, int W, bool MASKED, bool VEC>
-__global__ __launch_bounds__(64 * W) void fwd_general(Args a) {
-    using T = Tile<D>;
-    constexpr int NT = 64 * W;
-    constexpr int DB = D / 32;  // 32-column blocks of the head dimension
-    __shared__ __attribute__((aligned(16))) int8_t smem[T::BYTES];
-    int8_t* lk = smem;
-    int8_t* lvt = smem + T::KBYTES;
-
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
-    const int lq = lane & 31, g = lane >> 5;
-    const int zh = blockIdx.x / a.mblocks;
-    const int mb = blockIdx.x % a.mblocks;
-    const int z = zh / a.H, h = zh % a.H;
-    const int q0 = (mb * W + wave) * 32;
-    const bool active = q0 < a.N;
-
-    const int8_t* qb = a.q + z * a.sq[0] + h * a.sq[1];
-    const int8_t* kb = a.k + z * a.sk[0] + h * a.sk[1];
-    const int8_t* vb = a.v + z * a.sv[0] + h * a.sv[1];
-
-    // Q^T as the B operand: lane holds query q0+lq, head dims 32*db+16*g+[0,16).
-    i32x4 qv[DB];
-    const int qrow = q0 + lq;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-        qv[db] = load16<VEC>(qb + (int64_t)qrow * a.sq[2] + (int64_t)(db * 32 + g * 16) * a.sq[3], a.sq[3],
-                             qrow < a.N);
-
-    int32_t m = kNegInf, l = 1;  // kernel.py:138-139 (per query, S layout)
-    i32x16 acc[DB];              // kernel.py:140 (O layout)
-#pragma unroll
-    for (int t = 0; t < DB; ++t) acc[t] = i32x16{};
-
-    for (int kstart = 0; kstart < a.N; kstart += kBN) {  // kernel.py:147
-        __syncthreads();
-        stage_kv<D, NT, VEC>(a, kb, vb, kstart, lk, lvt, tid);
-        __syncthreads();
-        if (!active) continue;
-
-        // S^T = K . Q^T  (kernel.py:153); s[v] = S[q0+lq][kstart+crow(v,lane)]
-        i32x16 s = {};
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-            i32x4 kf = *reinterpret_cast<const i32x4*>(lk + lq * T::RK + db * 32 + g * 16);
-            s = mfma32(kf, qv[db], s);
-        }
-        int32_t mx = INT32_MIN;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            int key = kstart + crow(v, lane);
-            int32_t x = s[v];
-            if constexpr (MASKED) {  // kernel.py:250-253
-                if (key < a.N && qrow < a.N)
-                    x = wadd(x, a.bias[(a.bias_zmod ? z % a.bias_zmod : z) * a.sb[0] + h * a.sb[1] +
-                                       (int64_t)qrow * a.sb[2] + (int64_t)key * a.sb[3]]);
-            }
-            if (key >= a.N) x = kNegInf;  // kernel.py:154-156 (never true when N%32==0)
-            s[v] = x;
-            mx = max(mx, x);
-        }
-        mx = max(mx, __shfl_xor(mx, 32));
-        const int32_t mn = max(m, mx);  // kernel.py:158
-        int32_t lij = 0;
-        uint32_t pk[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {  // kernel.py:159-162
-            int32_t p = requant(exp2_i32(wsub(s[v], mn), a), a);
-            lij += p;
-            pk[v >> 2] |= ((uint32_t)p & 0xffu) << (8 * (v & 3));
-        }
-        lij += __shfl_xor(lij, 32);
-        const int32_t alpha = exp2_i32(wsub(m, mn), a);  // kernel.py:163
-        l = wadd(release(l, alpha, a.lM, a.l_shift, a.l_mode, a.rs), lij);  // kernel.py:164
-        // kernel.py:165 - rescale acc; acc row crow(v,lane) needs that row's alpha
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            int32_t av = __shfl(alpha, crow(v, lane));
-#pragma unroll
-            for (int t = 0; t < DB; ++t) acc[t][v] = release(acc[t][v], av, a.aM, a.acc_shift, a.acc_mode, a.rs);
-        }
-        // O += P . V  (kernel.py:171)
-        i32x4 pa = i32x4{(int32_t)pk[0], (int32_t)pk[1], (int32_t)pk[2], (int32_t)pk[3]};
-#pragma unroll
-        for (int t = 0; t < DB; ++t) {
-            i32x4 vf = *reinterpret_cast<const i32x4*>(lvt + (t * 32 + lq) * T::RV + g * 16);
-            acc[t] = mfma32(pa, vf, acc[t]);
-        }
-        m = mn;  // kernel.py:172
-    }
-    if (!active) return;
-    // kernel.py:176-180: fp32 divide, fp32->int32, int32->int8, rows < N only.
-    const __amdgpu_buffer_rsrc_t orsrc = out_rsrc(a, z, h, D);
-    const float os = a.out_dt == QFLASH_HIP_I8 ? 0.f : scale_value(a);
-    with_out_type(a.out_dt, [&]<int OUT>() {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int row = crow(v, lane);
-            const int32_t lv = __shfl(l, row);
-            const int orow = q0 + row;
-            if (orow >= a.N) continue;
-            const float lf = (float)lv;
-#pragma unroll
-            for (int t = 0; t < DB; ++t) {
-                int32_t code = cvt_x86(__fdiv_rn((float)acc[t][v], lf));
-                put_out<OUT>(orsrc, code, (int32_t)(orow * a.so[2] + (t * 32 + lq) * a.so[3]), 0, os);
-            }
-        }
-    });
-}
-
-// ----------------------------------------------------------------------------
-// Fast exact path.
-//
-// Valid when the host has proved (choose_path): shift exp variant, shift
-// rescale variants with shifts <= 30, eM <= 0, |eM| < 2^23, 0 < rs < 2^15,
-// |rM| < 2^23, |eM|*rs < 2^17, and for every real key column
-// |x| = |s - m'| <= X with X*|eM| <= 2^31 - 2^17 and the bound on |a| below
-// under 2^22 (unmasked: X = 2*D*2^14 from |s| <= D*128*128; masked: checked
-// per wave and step, general arithmetic otherwise).  Then q = (x*eM) >> 16 >= 0
-// never wraps and, with a = x + (q+2)*rs,
-//     E(x) = ((r >> 1) + rs) >> q  =  a >> min(q + 1, 31)        (r = x + q*rs)
-// which costs six VALU ops per score with 24-bit multiplies:
-//     t  = s*eM + c1          c1 = wrap32(-m'*eM) + 2^16   (t = x*eM + 2^16)
-//     q1 = t >> 16            (= q + 1)
-//     a  = s + q1*rs + c3     c3 = rs - m'
-//     E  = a >> min_u32(q1, 31)
-//     y  = E*rM + 2^15        p = int8(bits 16..23 of y)
-// Padded key columns (j >= N) use p(NEG_INF - m') evaluated exactly once per
-// row.  acc is rescaled only for rows whose running max changed (the rescale
-// by alpha = E(0) = rs is the identity while |acc*(rs*acc_M - 2^30)| < 2^29,
-// which the host proves from N), a register pair at a time, with one
-// 64-bit multiply-add per element.
-__device__ __forceinline__ int32_t mad24(int32_t a, int32_t b, int32_t c) { return __mul24(a, b) + c; }
-__device__ __forceinline__ int32_t max3(int32_t a, int32_t b, int32_t c) { return max(max(a, b), c); }
-__device__ __forceinline__ int32_t min3(int32_t a, int32_t b, int32_t c) { return min(min(a, b), c); }
-
-// K / V stages of 32 * STEPS keys (STEPS rescale steps) per LDS buffer.  Both tiles
-// hold rows of D bytes exactly as in HBM, copied there by buffer loads that
-// write LDS directly (no registers, no VALU), with the 16-byte chunks of each
-// row permuted by an XOR swizzle so that the MFMA operand reads are free of
-// bank conflicts:
-//   K: chunk c of key k sits at position c ^ kswz(k); lanes 0-7 of a
-//      ds_read_b128 read keys 0-7 at one chunk -> 8 distinct 4-bank groups;
-//   V: chunk c of key k sits at position c ^ vswz(k); V^T fragments are read
-//      with ds_read_b64_tr_b8, whose 16-lane groups read 8 keys x 2 halves of a
-//      chunk -> 16 distinct 2-bank groups.
-// Keys past N read as zeros (buffer range check), as the reference's
-// boundary-checked loads of K and V do.
-// Steps per stage: 4 at D = 64 with 4 waves per workgroup (one barrier per 128
-// keys; 2.3 % faster than 2 at ViT-B/384, and 36 KiB of LDS per workgroup
-// keeps 4 workgroups per CU); 2 otherwise, where the LDS of more, smaller
-// workgroups (D = 32 at 6 waves per SIMD, W < 4) or of D = 128 limits it.
-#ifdef QF_STAGE_STEPS
-template <int D, int W> constexpr int stage_steps() { return QF_STAGE_STEPS; }
-#else
-template <int D, int W> constexpr int stage_steps() { return D == 64 && W == 4 ? 4 : 2; }
-#endif
-template <int D, int W = 4>
-struct Stage {
-    static constexpr int STEPS = stage_steps<D, W>();  // 32-key rescale steps per stage
-    static_assert(STEPS >= 1 && STEPS <= 4, "stages of at most 128 keys (host offset check)");
-    static constexpr int KEYS = 32 * STEPS;
-    static constexpr int CPR = D / 16;       // 16-byte chunks per row
-    static constexpr int KBYTES = KEYS * D;  // one tile (K or V)
-    static constexpr int BYTES = 2 * KBYTES;
-    static constexpr int SLOTS = KEYS * CPR;  // 16-byte slots per tile
-    __device__ static int kswz(int k) {
-        return D == 32 ? (k >> 2) & 1 : (D == 64 ? (k >> 1) & 3 : k & 7);
-    }
-    __device__ static int vswz(int k) {
-        return D == 32 ? (k >> 3) & 1
-                       : (D == 64 ? ((k >> 1) & 1) | (((k >> 3) & 1) << 1) : (k & 3) | (((k >> 3) & 1) << 2));
-    }
-};
-
-// Per-lane byte offsets of the MFMA fragments inside a tile (keys 0-31 of it;
-// the second step of the stage adds 32*D).
-//   K (A operand of S^T = K.Q^T): key lq, chunk 2*db + g.
-//   V (B operand of O = P.V, read transposed): ds_read_b64_tr_b8 gives lane j
-//   of a 16-lane group byte (j & 7) of the 8-byte rows addressed by lanes
-//   2b + (j >> 3), b = 0..7.  Lane i = 2b + h of group G therefore addresses
-//   key 8(b>>2) + 4g + (b&3) (+16 for the fragment's second 8 bytes) and the
-//   8-byte unit 4t + 2(G&1) + h of the row, so that lane n + 32g receives
-//   column 32t + n of the 16 keys the P operand's byte order expects
-//   (byte 16g + b' <-> key 8(b'>>2) + 4g + (b'&3)).
-template <int D>
-struct Frag {
-    static constexpr int DB = D / 32;
-    int32_t k[DB], v[DB];
-    __device__ Frag(int lane) {
-        using S = Stage<D>;
-        const int lq = lane & 31, g = lane >> 5;
-        const int i = lane & 15, G = lane >> 4, b = i >> 1, h = i & 1;
-        const int kv = 8 * (b >> 2) + 4 * (G >> 1) + (b & 3);
-#pragma unroll
-        for (int db = 0; db < DB; ++db) k[db] = lq * D + 16 * ((2 * db + g) ^ S::kswz(lq));
-#pragma unroll
-        for (int t = 0; t < DB; ++t) {
-            const int u = 4 * t + 2 * (G & 1) + h;
-            v[t] = kv * D + 16 * ((u >> 1) ^ S::vswz(kv)) + 8 * (u & 1);
-        }
-    }
-};
-
-// V^T fragments of one step (B operands of O = P.V): two ds_read_b64_tr_b8
-// per 32-column block, the second 16 keys (16*D bytes) further.  Written as
-// one asm block with its own lgkmcnt wait: through the builtin, the compiler
-// would also wait for the in-flight copy of the NEXT stage (vmcnt(0)) before
-// every read, as it cannot tell the two LDS buffers apart.
-template <int D>
-__device__ __forceinline__ void read_vt(i32x4* vf, const int8_t* lv, const Frag<D>& fr) {
-    typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
-    const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)lv;
-    i32x2 r[2 * (D / 32)];
-    if constexpr (D == 32) {
-        asm volatile(
-            "ds_read_b64_tr_b8 %0, %2\n\t"
-            "ds_read_b64_tr_b8 %1, %2 offset:%c3\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=&v"(r[0]), "=&v"(r[1])
-            : "v"(base + fr.v[0]), "i"(16 * D));
-    } else if constexpr (D == 64) {
-        asm volatile(
-            "ds_read_b64_tr_b8 %0, %4\n\t"
-            "ds_read_b64_tr_b8 %1, %4 offset:%c6\n\t"
-            "ds_read_b64_tr_b8 %2, %5\n\t"
-            "ds_read_b64_tr_b8 %3, %5 offset:%c6\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
-            : "v"(base + fr.v[0]), "v"(base + fr.v[1]), "i"(16 * D));
-    } else {
-        asm volatile(
-            "ds_read_b64_tr_b8 %0, %8\n\t"
-            "ds_read_b64_tr_b8 %1, %8 offset:%c12\n\t"
-            "ds_read_b64_tr_b8 %2, %9\n\t"
-            "ds_read_b64_tr_b8 %3, %9 offset:%c12\n\t"
-            "ds_read_b64_tr_b8 %4, %10\n\t"
-            "ds_read_b64_tr_b8 %5, %10 offset:%c12\n\t"
-            "ds_read_b64_tr_b8 %6, %11\n\t"
-            "ds_read_b64_tr_b8 %7, %11 offset:%c12\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]),
-              "=&v"(r[7])
-            : "v"(base + fr.v[0]), "v"(base + fr.v[1]), "v"(base + fr.v[2]), "v"(base + fr.v[3]), "i"(16 * D));
-    }
-#pragma unroll
-    for (int t = 0; t < D / 32; ++t) vf[t] = i32x4{r[2 * t].x, r[2 * t].y, r[2 * t + 1].x, r[2 * t + 1].y};
-}
-
-// Direct HBM -> LDS copies of one stage: slot s of a tile (16 bytes at byte
-// 16*s) holds chunk (s % CPR) ^ swz(key) of key s / CPR; wave w of the
-// workgroup fills slots [r*NT + 64w, r*NT + 64w + 64) in round r.
-template <int D, int W>
-struct StageDma {
-    using S = Stage<D, W>;
-    static constexpr int NT = 64 * W;
-    static constexpr int R = (S::SLOTS + NT - 1) / NT;
-    uint32_t vk[R], vv[R];
-    __device__ StageDma(const Args& a, int wave, int lane) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int slot = r * NT + wave * 64 + lane;
-            const int key = slot / S::CPR, pos = slot % S::CPR;
-            vk[r] = (uint32_t)(key * (int32_t)a.sk[2] + 16 * (pos ^ S::kswz(key)));
-            vv[r] = (uint32_t)(key * (int32_t)a.sv[2] + 16 * (pos ^ S::vswz(key)));
-        }
-    }
-    __device__ void issue(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv, int8_t* buf, int kstart,
-                          const Args& a, int wave) const {
-        const uint32_t sk = (uint32_t)(kstart * (int32_t)a.sk[2]), sv = (uint32_t)(kstart * (int32_t)a.sv[2]);
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if (r * NT + wave * 64 < S::SLOTS) {
-                int8_t* lk = buf + (r * NT + wave * 64) * 16;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)lk, 16, vk[r],
-                                                         sk, 0, 0);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    rv, (__attribute__((address_space(3))) void*)(lk + S::KBYTES), 16, vv[r], sv, 0, 0);
-            }
-        }
-    }
-};
-
-// Completion of this wave's LDS copies (vmcnt), then the workgroup barrier.
-__device__ __forceinline__ void stage_sync() {
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __syncthreads();
-}
-
-// Workgroup id -> (head, query block) so that consecutive blocks of one head
-// run on the same XCD (workgroups are dealt to the 8 XCDs round-robin).
-__device__ __forceinline__ int xcd_order(int b, int n) {
-    const int per = n >> 3, rem = n & 7, x = b & 7, i = b >> 3;
-    return x < rem ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
-}
-
-__device__ __forceinline__ int32_t rescale_fast(int32_t x, int32_t A, int64_t half, int32_t sh) {
-    const int64_t p = (int64_t)x * (int64_t)A + half;
-    return (int32_t)__builtin_amdgcn_alignbit((uint32_t)(p >> 32), (uint32_t)p, (uint32_t)sh);
-}
-
-// Value of the other lane-half (lane ^ 32) combined with this lane's: the
-// two results of v_permlane32_swap are {this, other} in some order.
-__device__ __forceinline__ int32_t half_max(int32_t v) {
-    const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
-    return max((int32_t)r[0], (int32_t)r[1]);
-}
-__device__ __forceinline__ int32_t half_sum(int32_t v) {
-    const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
-    return (int32_t)(r[0] + r[1]);
-}
-__device__ __forceinline__ int32_t half_min(int32_t v) {
-    const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
-    return min((int32_t)r[0], (int32_t)r[1]);
-}
-// ds_bpermute_b32 with the lane's byte address split into a register and an
-// immediate offset: through the builtin the compiler hoists the 16 distinct
-// addresses of the rescale out of the loop and holds 16 VGPRs for them.
-template <int OFF>
-__device__ __forceinline__ int32_t bpermute_off(int32_t addr, int32_t v) {
-    int32_t r;
-    asm volatile("ds_bpermute_b32 %0, %1, %2 offset:%3\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr), "v"(v), "i"(OFF));
-    return r;
-}
-// Keeps the compiler from distributing a per-row constant back into the
-// per-element expressions (it would turn one mad into mul + sub + add).
-__device__ __forceinline__ int32_t opaque(int32_t v) {
-    asm volatile("" : "+v"(v));
-    return v;
-}
-
-// E(x) for one x <= 0 inside the fast path's range (see the comment above).
-__device__ __forceinline__ int32_t exp2_fast(int32_t x, int32_t eM, int32_t rs) {
-    const int32_t t = mad24(x, eM, 1 << 16);
-    const int32_t q1 = t >> 16;
-    const int32_t av = x + __mul24(q1, rs) + rs;
-    return av >> min((uint32_t)q1, 31u);
-}
-
-// exp2 + requantisation by table lookup.  For x = s - m' = -u the
-// reference's p(x) = int8(requant(exp2(x))) depends on u alone, and past a
-// host-computed point it is 0 over a long range: with q = floor(u*|eM| / 2^16)
-// (no int32 wrap while u*|eM| < 2^31) and kappa = |eM|*rs - 2^16, the
-// remainder r = q*rs - u lies in (u*kappa/2^16 - rs, u*kappa/2^16], so
-// E = ((r >> 1) + rs) >> q is 0 once 2^q exceeds rs + max(0, r/2) (true for
-// q >= bitlen(rs) + 3 when kappa <= 2|eM|) as long as r >= -2rs (all u when
-// kappa >= 0, u <= rs*2^16/|kappa| otherwise); p(E = 0) = 0.  The table holds
-// p(u) for u = 0 .. lut_n - 1 (its last entry 0) in reverse order, entry
-// j = lut_n - 1 - u, so that the index of every u up to lut_lim is
-// max(s - thr, 0) with thr = m' - (lut_n - 1): one saturating subtraction per
-// score when scores and thr are positive (kScoreBias), a subtraction and a
-// max otherwise.  A step uses the table only when all of its real columns
-// have u <= lut_lim.  Clamping also makes the many far-off columns of a step
-// read one byte (a broadcast, no LDS bank conflict): with the addresses left
-// spread over a table of 8 KB the kernel is slower (measured).  The table
-// lives in LDS after the K / V stages, at the compile-time LDS address LUT
-// (the kernel's only LDS array starts at address 0; the kernel checks it),
-// which the byte loads take as their immediate offset.  Each byte load fills
-// bits 0-7 of its own register (the half-register d16 loads are no use here:
-// with SRAM ECC on, as on MI355X, they clear the other half), and three
-// shift-ors pack four p values into the MFMA A operand's byte order.  The
-// step's V^T fragment reads (read_vt) go out in the same asm block, so one
-// LDS wait covers both; the compiler's own packing of byte loads would take
-// 4.5 instructions per four bytes, and it would wait for the in-flight
-// stage copy before every LDS read.
-#define QF_LUT_LOADS                                   \
-    "ds_read_u8 %0, %0 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %1, %1 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %2, %2 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %3, %3 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %4, %4 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %5, %5 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %6, %6 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %7, %7 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %8, %8 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %9, %9 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %10, %10 offset:%c[lut]\n\t"           \
-    "ds_read_u8 %11, %11 offset:%c[lut]\n\t"           \
-    "ds_read_u8 %12, %12 offset:%c[lut]\n\t"           \
-    "ds_read_u8 %13, %13 offset:%c[lut]\n\t"           \
-    "ds_read_u8 %14, %14 offset:%c[lut]\n\t"           \
-    "ds_read_u8 %15, %15 offset:%c[lut]\n\t"
-#define QF_LUT_PACK                                    \
-    "s_waitcnt lgkmcnt(0)\n\t"                          \
-    "v_lshl_or_b32 %0, %1, 8, %0\n\t"                   \
-    "v_lshl_or_b32 %2, %3, 8, %2\n\t"                   \
-    "v_lshl_or_b32 %0, %2, 16, %0\n\t"                  \
-    "v_lshl_or_b32 %4, %5, 8, %4\n\t"                   \
-    "v_lshl_or_b32 %6, %7, 8, %6\n\t"                   \
-    "v_lshl_or_b32 %4, %6, 16, %4\n\t"                  \
-    "v_lshl_or_b32 %8, %9, 8, %8\n\t"                   \
-    "v_lshl_or_b32 %10, %11, 8, %10\n\t"                \
-    "v_lshl_or_b32 %8, %10, 16, %8\n\t"                 \
-    "v_lshl_or_b32 %12, %13, 8, %12\n\t"                \
-    "v_lshl_or_b32 %14, %15, 8, %14\n\t"                \
-    "v_lshl_or_b32 %12, %14, 16, %12"
-#define QF_LUT_IDX_OPERANDS                                                                                  \
-    "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),         \
-        "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]), "+v"(r[12]), "+v"(r[13]), "+v"(r[14]), "+v"(r[15])
-
-template <int D, int LUT>
-__device__ __forceinline__ void lut_pack_vt(uint32_t* pk, i32x4* vf, const uint32_t* idx, const int8_t* lv,
-                                            const Frag<D>& fr) {
-    static_assert(LUT >= 0 && LUT + kLutMax <= 65536, "table offset must fit the 16-bit LDS immediate");
-    typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
-    const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)lv;
-    // each byte load writes its result over its own index register
-    uint32_t r[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) r[i] = idx[i];
-    i32x2 t[2 * (D / 32)];
-    if constexpr (D == 32) {
-        asm volatile(QF_LUT_LOADS
-                     "ds_read_b64_tr_b8 %[t0], %[b0]\n\t"
-                     "ds_read_b64_tr_b8 %[t1], %[b0] offset:%c[vo]\n\t" QF_LUT_PACK
-                     : QF_LUT_IDX_OPERANDS, [t0] "=&v"(t[0]), [t1] "=&v"(t[1])
-                     : [b0] "v"(base + fr.v[0]), [vo] "i"(16 * D), [lut] "i"(LUT));
-    } else if constexpr (D == 64) {
-        asm volatile(QF_LUT_LOADS
-                     "ds_read_b64_tr_b8 %[t0], %[b0]\n\t"
-                     "ds_read_b64_tr_b8 %[t1], %[b0] offset:%c[vo]\n\t"
-                     "ds_read_b64_tr_b8 %[t2], %[b1]\n\t"
-                     "ds_read_b64_tr_b8 %[t3], %[b1] offset:%c[vo]\n\t" QF_LUT_PACK
-                     : QF_LUT_IDX_OPERANDS, [t0] "=&v"(t[0]), [t1] "=&v"(t[1]), [t2] "=&v"(t[2]), [t3] "=&v"(t[3])
-                     : [b0] "v"(base + fr.v[0]), [b1] "v"(base + fr.v[1]), [vo] "i"(16 * D), [lut] "i"(LUT));
-    } else {
-        asm volatile(QF_LUT_LOADS
-                     "ds_read_b64_tr_b8 %[t0], %[b0]\n\t"
-                     "ds_read_b64_tr_b8 %[t1], %[b0] offset:%c[vo]\n\t"
-                     "ds_read_b64_tr_b8 %[t2], %[b1]\n\t"
-                     "ds_read_b64_tr_b8 %[t3], %[b1] offset:%c[vo]\n\t"
-                     "ds_read_b64_tr_b8 %[t4], %[b2]\n\t"
-                     "ds_read_b64_tr_b8 %[t5], %[b2] offset:%c[vo]\n\t"
-                     "ds_read_b64_tr_b8 %[t6], %[b3]\n\t"
-                     "ds_read_b64_tr_b8 %[t7], %[b3] offset:%c[vo]\n\t" QF_LUT_PACK
-                     : QF_LUT_IDX_OPERANDS, [t0] "=&v"(t[0]), [t1] "=&v"(t[1]), [t2] "=&v"(t[2]), [t3] "=&v"(t[3]),
-                       [t4] "=&v"(t[4]), [t5] "=&v"(t[5]), [t6] "=&v"(t[6]), [t7] "=&v"(t[7])
-                     : [b0] "v"(base + fr.v[0]), [b1] "v"(base + fr.v[1]), [b2] "v"(base + fr.v[2]),
-                       [b3] "v"(base + fr.v[3]), [vo] "i"(16 * D), [lut] "i"(LUT));
-    }
-#pragma unroll
-    for (int w = 0; w < 4; ++w) pk[w] = r[4 * w];
-#pragma unroll
-    for (int i = 0; i < D / 32; ++i) vf[i] = i32x4{t[2 * i].x, t[2 * i].y, t[2 * i + 1].x, t[2 * i + 1].y};
-}
-// The first TV score registers only (TV = 4, 8, 12: a partial last step of at
-// most 2*TV keys, whose registers TV..15 hold padded columns alone): pk[0 ..
-// TV/4 - 1] (the others 0) and the V^T fragments.
-#define QF_L(i) "ds_read_u8 %" #i ", %" #i " offset:%c[lut]\n\t"
-#define QF_P(a, b, c, d)                                      \
-    "v_lshl_or_b32 %" #a ", %" #b ", 8, %" #a "\n\t"            \
-    "v_lshl_or_b32 %" #c ", %" #d ", 8, %" #c "\n\t"            \
-    "v_lshl_or_b32 %" #a ", %" #c ", 16, %" #a "\n\t"
-#define QF_LOADS4 QF_L(0) QF_L(1) QF_L(2) QF_L(3)
-#define QF_LOADS8 QF_LOADS4 QF_L(4) QF_L(5) QF_L(6) QF_L(7)
-#define QF_LOADS12 QF_LOADS8 QF_L(8) QF_L(9) QF_L(10) QF_L(11)
-#define QF_PACK4 "s_waitcnt lgkmcnt(0)\n\t" QF_P(0, 1, 2, 3)
-#define QF_PACK8 QF_PACK4 QF_P(4, 5, 6, 7)
-#define QF_PACK12 QF_PACK8 QF_P(8, 9, 10, 11)
-#define QF_IDX4 "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3])
-#define QF_IDX8 QF_IDX4, "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7])
-#define QF_IDX12 QF_IDX8, "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11])
-#define QF_TR32                                           \
-    "ds_read_b64_tr_b8 %[t0], %[b0]\n\t"                  \
-    "ds_read_b64_tr_b8 %[t1], %[b0] offset:%c[vo]\n\t"
-#define QF_TR64 QF_TR32                                   \
-    "ds_read_b64_tr_b8 %[t2], %[b1]\n\t"                  \
-    "ds_read_b64_tr_b8 %[t3], %[b1] offset:%c[vo]\n\t"
-#define QF_TR128 QF_TR64                                  \
-    "ds_read_b64_tr_b8 %[t4], %[b2]\n\t"                  \
-    "ds_read_b64_tr_b8 %[t5], %[b2] offset:%c[vo]\n\t"    \
-    "ds_read_b64_tr_b8 %[t6], %[b3]\n\t"                  \
-    "ds_read_b64_tr_b8 %[t7], %[b3] offset:%c[vo]\n\t"
-#define QF_T32 [t0] "=&v"(t[0]), [t1] "=&v"(t[1])
-#define QF_T64 QF_T32, [t2] "=&v"(t[2]), [t3] "=&v"(t[3])
-#define QF_T128 QF_T64, [t4] "=&v"(t[4]), [t5] "=&v"(t[5]), [t6] "=&v"(t[6]), [t7] "=&v"(t[7])
-#define QF_B32 [b0] "v"(base + fr.v[0]), [vo] "i"(16 * D), [lut] "i"(LUT)
-#define QF_B64 QF_B32, [b1] "v"(base + fr.v[1])
-#define QF_B128 QF_B64, [b2] "v"(base + fr.v[2]), [b3] "v"(base + fr.v[3])
-#define QF_TV_ASM(LOADS, PACK, IDX)                                                             \
-    if constexpr (D == 32)                                                                      \
-        asm volatile(LOADS QF_TR32 PACK : IDX, QF_T32 : QF_B32);                                \
-    else if constexpr (D == 64)                                                                 \
-        asm volatile(LOADS QF_TR64 PACK : IDX, QF_T64 : QF_B64);                                \
-    else                                                                                        \
-        asm volatile(LOADS QF_TR128 PACK : IDX, QF_T128 : QF_B128);
-template <int D, int LUT, int TV>
-__device__ __forceinline__ void lut_pack_vtn(uint32_t* pk, i32x4* vf, const uint32_t* idx, const int8_t* lv,
-                                             const Frag<D>& fr) {
-    static_assert(LUT >= 0 && LUT + kLutMax <= 65536, "table offset must fit the 16-bit LDS immediate");
-    static_assert(TV == 4 || TV == 8 || TV == 12, "4, 8 or 12 registers");
-    typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
-    const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)lv;
-    uint32_t r[TV];
-#pragma unroll
-    for (int i = 0; i < TV; ++i) r[i] = idx[i];
-    i32x2 t[2 * (D / 32)];
-    if constexpr (TV == 4) {
-        QF_TV_ASM(QF_LOADS4, QF_PACK4, QF_IDX4)
-    } else if constexpr (TV == 8) {
-        QF_TV_ASM(QF_LOADS8, QF_PACK8, QF_IDX8)
-    } else {
-        QF_TV_ASM(QF_LOADS12, QF_PACK12, QF_IDX12)
-    }
-#pragma unroll
-    for (int w = 0; w < 4; ++w) pk[w] = 4 * w < TV ? r[4 * w < TV ? 4 * w : 0] : 0u;
-#pragma unroll
-    for (int i = 0; i < D / 32; ++i) vf[i] = i32x4{t[2 * i].x, t[2 * i].y, t[2 * i + 1].x, t[2 * i + 1].y};
-}
-#undef QF_L
-#undef QF_P
-#undef QF_LOADS4
-#undef QF_LOADS8
-#undef QF_LOADS12
-#undef QF_PACK4
-#undef QF_PACK8
-#undef QF_PACK12
-#undef QF_IDX4
-#undef QF_IDX8
-#undef QF_IDX12
-#undef QF_TR32
-#undef QF_TR64
-#undef QF_TR128
-#undef QF_T32
-#undef QF_T64
-#undef QF_T128
-#undef QF_B32
-#undef QF_B64
-#undef QF_B128
-#undef QF_TV_ASM
-#undef QF_LUT_LOADS
-#undef QF_LUT_PACK
-#undef QF_LUT_IDX_OPERANDS
-
-// Per-wave state of the fast kernel (S layout for m, l, bnd: lane = query;
-// O layout for acc).
-template <int D>
-struct FastState {
-    static constexpr int DB = D / 32;
-    i32x16 acc[DB];
-    int32_t m, l;
-    float bnd;  // per-row upper bound on max_d |acc| (dynamic identity proof)
-    int wide;   // sticky: an alpha*acc_M left int32 -> every row is rescaled exactly
-};
-
-// Bias row of one query (kernel.py:232-236, :253) for the masked fast kernel.
-// With unit key stride the 16 values of a lane (keys 8k + 4g + [0, 4) of the
-// step) are four 16-byte buffer loads at lane-constant offsets; keys or rows
-// past the head's bias extent read as 0 (their scores are replaced anyway).
-struct BiasRow {
-    __amdgpu_buffer_rsrc_t rsrc;
-    int32_t voff;        // bytes: (row * sb2 + 4g) * 4
-    const int32_t* row;  // strided fallback (nullptr for rows >= N)
-};
-
-template <bool TAIL>
-__device__ __forceinline__ void load_bias(int32_t* bias_v, const Args& a, const BiasRow& br, int kstart, int lane) {
-    if (a.bias_vec) {
-#pragma unroll
-        for (int k4 = 0; k4 < 4; ++k4) {
-            const i32x4 b = __builtin_bit_cast(
-                i32x4, __builtin_amdgcn_raw_buffer_load_b128(br.rsrc, br.voff + 32 * k4, 4 * kstart, 0));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) bias_v[4 * k4 + e] = b[e];
-        }
-    } else {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int key = kstart + crow(v, lane);
-            bias_v[v] = ((!TAIL || key < a.N) && br.row) ? br.row[(int64_t)key * a.sb[3]] : 0;
-        }
-    }
-}
-
-// max / min over the first TV score registers (three-input chains)
-template <int TV>
-__device__ __forceinline__ int32_t max_first(const i32x16& s) {
-    int32_t m = TV == 1 ? s[0] : max(s[0], s[1]);
-#pragma unroll
-    for (int v = 2; v + 1 < TV; v += 2) m = max3(m, s[v], s[v + 1]);
-    if constexpr (TV > 2 && TV % 2) m = max(m, s[TV - 1]);
-    return m;
-}
-template <int TV>
-__device__ __forceinline__ int32_t min_first(const i32x16& s) {
-    int32_t m = TV == 1 ? s[0] : min(s[0], s[1]);
-#pragma unroll
-    for (int v = 2; v + 1 < TV; v += 2) m = min3(m, s[v], s[v + 1]);
-    if constexpr (TV > 2 && TV % 2) m = min(m, s[TV - 1]);
-    return m;
-}
-
-// S^T tile of one step with bias and padding applied (kernel.py:153-156, :250-253);
-// returns the row max over the 32 columns (both lane halves).
-// smin: the minimum over the real columns when MASKED or need_min (else INT32_MAX).
-// Unmasked: every score carries kScoreBias, from an extra MFMA of xb (all
-// bytes -128) with itself.  TV < 16 (partial steps of at most 2*TV keys):
-// registers TV..15 hold padded columns only and are set to the padding value.
-template <int D, bool MASKED, bool TAIL, int TV = 16>
-__device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& a, const i32x4* qv,
-                                          const int8_t* lk, const Frag<D>& fr, const int32_t* bias_v, int kstart,
-                                          int lane, bool need_min, i32x4 xb) {
-    constexpr int DB = D / 32;
-    constexpr int32_t PAD = kNegInf + (MASKED ? 0 : kScoreBias);
-    // K fragments first: the bias MFMA runs while they are in flight
-    i32x4 kf[DB];
-#pragma unroll
-    for (int db = 0; db < DB; ++db) kf[db] = *reinterpret_cast<const i32x4*>(lk + fr.k[db]);
-    if constexpr (MASKED)
-        s = i32x16{};
-    else
-        s = mfma32(xb, xb, i32x16{});
-#pragma unroll
-    for (int db = 0; db < DB; ++db) s = mfma32(kf[db], qv[db], s);
-    smin = INT32_MAX;
-    const int32_t tcut = a.N - kstart - 4 * (lane >> 5);
-    if constexpr (MASKED) {
-#pragma unroll
-        for (int v = 0; v < TV; ++v) {
-            s[v] = wadd(s[v], bias_v[v]);
-            if (!TAIL || !padded(v, tcut)) smin = min(smin, s[v]);
-        }
-    } else if (need_min) {
-        // over the raw scores: a padded column's raw score (its K row reads as
-        // 0) is the bias alone, which can only lower the minimum, so a check
-        // that passes with it passes for the real columns
-        smin = min_first<TV>(s);
-    }
-    if constexpr (TAIL) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v)
-            if (v >= TV || padded(v, tcut)) s[v] = PAD;
-    }
-    return half_max(max_first<TV>(s));
-}
-
-// One 32-key step (qflash/kernel.py:147-174) for the 32 query rows of a wave.
-// Every branch below is wave-uniform and none of them holds an alternative
-// computation of acc (the accumulators keep their registers across steps).
-// Scores, m and m' carry the bias SB (kScoreBias when unmasked): only their
-// differences enter the arithmetic.  LUT: LDS address of the p table.
-template <int D, int LUT, bool MASKED, bool TAIL, bool WIDE, bool DYN, bool FIRST, int TV = 16>
-__device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const i32x4* qv, const int8_t* lk,
-                                          const int8_t* lv, const Frag<D>& fr, const BiasRow& brow, int kstart,
-                                          int lane, bool wave_fast, int32_t xlim, int lut_mode, i32x4 xb) {
-    constexpr int DB = D / 32;
-    constexpr int32_t SB = MASKED ? 0 : kScoreBias;
-    const int g = lane >> 5;
-    const int32_t rs = a.rs, eM = a.eM, rM = a.rM;
-
-    int32_t bias_v[16];
-    if constexpr (MASKED) load_bias<TAIL>(bias_v, a, brow, kstart, lane);
-    i32x16 s;
-    int32_t smin;
-    static_assert(TV == 16 || (TAIL && (TV == 4 || TV == 8 || TV == 12)), "TV < 16: partial steps of <= 2*TV keys");
-    const int32_t mx = scores<D, MASKED, TAIL, TV>(s, smin, a, qv, lk, fr, bias_v, kstart, lane, lut_mode == 2, xb);
-    const int32_t m = st.m;
-    const int32_t mn = max(m, mx);  // kernel.py:158
-    const int32_t dm = wsub(m, mn);
-    constexpr bool first = FIRST;  // kstart == 0
-
-    // Each lane half checks its own minimum against the row's mn (the checks
-    // below are wave-wide); a masked partial step's half may have no real
-    // column (minimum INT32_MAX) and takes the other half's.
-    if constexpr (MASKED && TAIL) smin = half_min(smin);
-    // table path: every real column of the wave has u = m' - s <= lut_lim
-    // (lut_mode 1: proved for the whole row block from ||q||_1)
-    // (mn >= smin: the difference is exact as an unsigned 32-bit value)
-    const bool lut_ok = lut_mode == 1 || (lut_mode == 2 && __all((uint32_t)(mn - smin) <= (uint32_t)a.lut_lim));
-    bool vec_ok = wave_fast;
-    if constexpr (MASKED)
-        vec_ok = vec_ok && __all(smin > -(1 << 23) && mn < (1 << 23) && (int64_t)mn - smin <= xlim);
-    uint32_t pk[4];
-    i32x4 vf[DB];
-    if (lut_ok) {
-        // table index max(s - thr, 0) = lut_n - 1 - min(u, lut_n - 1)
-        const int32_t thr = wsub(mn, a.lut_n - 1);
-        uint32_t idx[16];
-        if constexpr (MASKED) {
-            // real columns: s - thr = lut_n - 1 - u >= lut_n - 1 - lut_lim > INT32_MIN, no wrap
-#pragma unroll
-            for (int v = 0; v < TV; ++v) idx[v] = (uint32_t)max(wsub(s[v], thr), 0);
-        } else {
-            // scores and thr in [1, 2^31) (lut_mode != 0 only then): unsigned saturation
-#pragma unroll
-            for (int v = 0; v < TV; ++v) idx[v] = __builtin_elementwise_sub_sat((uint32_t)s[v], (uint32_t)thr);
-        }
-        if constexpr (TAIL) {  // padded columns read entry 0 (p = 0); l gets their p below
-            const int32_t tcut = a.N - kstart - 4 * g;
-#pragma unroll
-            for (int v = 0; v < TV; ++v)
-                if (padded(v, tcut)) idx[v] = 0;
-        }
-        if constexpr (TV < 16)
-            lut_pack_vtn<D, LUT, TV>(pk, vf, idx, lv, fr);
-        else
-            lut_pack_vt<D, LUT>(pk, vf, idx, lv, fr);
-    } else if (vec_ok) {
-        // kernel.py:159-161 in six ops per score (see the fast-path comment)
-        const int32_t c1 = opaque(wadd(wmul(wsub(0, mn), eM), 1 << 16));
-        const int32_t c3 = opaque(wsub(rs, mn));
-        const int32_t c15 = opaque(1 << 15);
-#pragma unroll
-        for (int v = 0; v < TV; ++v) {  // registers TV..15 are padded columns (set below)
-            const int32_t t = mad24(s[v], eM, c1);
-            const int32_t q1 = t >> 16;
-            const int32_t av = s[v] + __mul24(q1, rs) + c3;
-            const int32_t E = av >> min((uint32_t)q1, 31u);
-            s[v] = mad24(E, rM, c15);  // p = bits 16..23
-        }
-        if constexpr (TAIL) {  // padded key columns: p(NEG_INF - m') exactly, once per row
-            const int32_t ppad = (int32_t)((uint32_t)requant(exp2_i32(wsub(kNegInf + SB, mn), a), a) << 16);
-            const int32_t tcut = a.N - kstart - 4 * g;
-#pragma unroll
-            for (int v = 0; v < 16; ++v)
-                if (padded(v, tcut)) s[v] = ppad;
-        }
-#pragma unroll
-        for (int w4 = 0; w4 < 4; ++w4) {
-            const uint32_t lo = __builtin_amdgcn_perm((uint32_t)s[4 * w4 + 1], (uint32_t)s[4 * w4], 0x0c0c0602u);
-            const uint32_t hi = __builtin_amdgcn_perm((uint32_t)s[4 * w4 + 3], (uint32_t)s[4 * w4 + 2], 0x0c0c0602u);
-            pk[w4] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
-        }
-    } else {  // general exact arithmetic for this step's scores (p in bits 0-7)
-        // One score at a time through a rotating queue: this rare path then holds
-        // the temporaries of one evaluation only, not of sixteen interleaved ones.
-#pragma unroll 1
-        for (int i = 0; i < 16; ++i) {
-            const int32_t pv = requant(exp2_i32(wsub(s[0], mn), a), a);
-#pragma unroll
-            for (int v = 0; v < 15; ++v) s[v] = s[v + 1];
-            s[15] = pv;
-        }
-#pragma unroll
-        for (int w4 = 0; w4 < 4; ++w4) {
-            const uint32_t lo = __builtin_amdgcn_perm((uint32_t)s[4 * w4 + 1], (uint32_t)s[4 * w4], 0x0c0c0400u);
-            const uint32_t hi = __builtin_amdgcn_perm((uint32_t)s[4 * w4 + 3], (uint32_t)s[4 * w4 + 2], 0x0c0c0400u);
-            pk[w4] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
-        }
-    }
-    // kernel.py:162
-    int32_t lij = __builtin_amdgcn_sdot4((int)pk[0], 0x01010101, 0, false);
-    lij = __builtin_amdgcn_sdot4((int)pk[1], 0x01010101, lij, false);
-    lij = __builtin_amdgcn_sdot4((int)pk[2], 0x01010101, lij, false);
-    lij = __builtin_amdgcn_sdot4((int)pk[3], 0x01010101, lij, false);
-    lij = half_sum(lij);
-    if constexpr (TAIL) {
-        // Table path of the last, partial step: the padded columns (score
-        // NEG_INF) read p = 0; their P.V term is 0 anyway (V rows past N read
-        // as 0), so only l needs their exact p.
-        if (lut_ok) lij = wadd(lij, (32 - (a.N - kstart)) * requant(exp2_i32(wsub(kNegInf + SB, mn), a), a));
-    }
-
-    // kernel.py:163-165
-    int32_t alpha;
-    bool wide_step;
-    if constexpr (!WIDE) {
-        // Unmasked fast waves: past the first step m and m' are maxima of real
-        // scores, so |m - m'| <= 2*smax <= X and alpha = E(m - m') is in [-1, rs].
-        // The first step's alpha may be anything, but acc is still 0 then.
-        alpha = first ? exp2_i32(dm, a) : exp2_fast(dm, eM, rs);
-        wide_step = first;
-    } else {
-        if (!first && wave_fast && __all(-dm <= xlim))
-            alpha = exp2_fast(dm, eM, rs);  // in [-1, rs]
-        else
-            alpha = exp2_i32(dm, a);        // in [-1, rs] unless dm*eM overflows
-        // rs*l_M and rs*acc_M < 2^31 (host): alpha in [-rs, rs] keeps both multipliers in int32
-        wide_step = !__all(alpha >= -rs && alpha <= rs);
-        if (!first && wide_step) st.wide = 1;
-    }
-    if (!wide_step) {
-        const int64_t pl = (int64_t)st.l * (int64_t)wmul(alpha, a.lM) + (1ll << (a.l_shift - 1));
-        st.l = wadd((int32_t)__builtin_amdgcn_alignbit((uint32_t)(pl >> 32), (uint32_t)pl, (uint32_t)a.l_shift),
-                    lij);
-    } else {
-        st.l = wadd(release(st.l, alpha, a.lM, a.l_shift, 1, rs), lij);
-    }
-    const int64_t A64 = (int64_t)alpha * a.aM;
-    const int32_t A = (int32_t)A64;
-    // high word of A64 once A's sign is extended (zero unless A64 leaves int32)
-    const int32_t Ah = (int32_t)(A64 >> 32) + (int32_t)((uint32_t)A >> 31);
-    const int32_t as = a.acc_shift;
-    if (!first) {  // acc == 0 before the first step: its rescale is 0 for any alpha
-        bool need = mn != m;
-        if constexpr (DYN) need = need || st.bnd * (float)a.e_acc >= __builtin_ldexpf(0.99f, as - 1);
-        uint32_t chg = __builtin_amdgcn_readfirstlane((uint32_t)__ballot(need));
-        int wide = 0;
-        if constexpr (WIDE) wide = __builtin_amdgcn_readfirstlane(st.wide);
-        if (wide) chg = 0xffffffffu;  // the identity proof no longer holds: rescale every row
-        if constexpr (DYN)
-            if (need || wide)
-                st.bnd = __builtin_fmaf(st.bnd * (fabsf((float)alpha) * (float)a.aM * __builtin_ldexpf(1.f, -as)),
-                                        1.0000010f, 1.f);
-        if (chg) {
-            // register pair v = rows rlo (lanes 0-31) and rlo+4 (lanes 32-63) of the O layout;
-            // the multiplier of row r sits in lane r of the S layout.
-            // acc*A64 + 2^(as-1) mod 2^64 = acc*sext(A) + 2^(as-1) + (acc*Ah << 32)
-            const int64_t ahalf = 1ll << (as - 1);
-            const int addr = g * 16;
-            // bit rlo: row rlo or rlo + 4 changed (one scalar bit test per pair)
-            const uint32_t pairs = (chg | (chg >> 4)) & 0x0F0F0F0Fu;
-            auto pair = [&]<int V>() {
-                constexpr int rlo = 8 * (V >> 2) + (V & 3);
-                if ((pairs >> rlo) & 1u) {
-                    const int32_t av = bpermute_off<4 * rlo>(addr, A);
-                    int32_t ah = 0;
-                    if constexpr (WIDE) ah = wide ? bpermute_off<4 * rlo>(addr, Ah) : 0;
-#pragma unroll
-                    for (int t = 0; t < DB; ++t) {
-                        const int64_t p = (int64_t)st.acc[t][V] * (int64_t)av + ahalf;
-                        uint32_t hi = (uint32_t)(p >> 32);
-                        if constexpr (WIDE)
-                            if (wide) hi += (uint32_t)wmul(st.acc[t][V], ah);
-                        st.acc[t][V] = (int32_t)__builtin_amdgcn_alignbit(hi, (uint32_t)p, (uint32_t)as);
-                    }
-                }
-            };
-            [&]<int... V>(std::integer_sequence<int, V...>) { (pair.template operator()<V>(), ...); }(
-                std::make_integer_sequence<int, 16>{});
-        }
-    }
-    if constexpr (DYN) {  // |P.V| <= 128 * sum|p|, and sum|p| <= sum of the bytes read as unsigned
-        uint32_t sa = __builtin_amdgcn_udot4(pk[0], 0x01010101u, 0u, false);
-        sa = __builtin_amdgcn_udot4(pk[1], 0x01010101u, sa, false);
-        sa = __builtin_amdgcn_udot4(pk[2], 0x01010101u, sa, false);
-        sa = __builtin_amdgcn_udot4(pk[3], 0x01010101u, sa, false);
-        sa = (uint32_t)half_sum((int32_t)sa);
-        st.bnd = (st.bnd + 128.f * (float)sa) * 1.0000010f;
-    }
-    // O += P . V (kernel.py:171)
-    const i32x4 pa = i32x4{(int32_t)pk[0], (int32_t)pk[1], (int32_t)pk[2], (int32_t)pk[3]};
-    if (!lut_ok) read_vt<D>(vf, lv, fr);
-#pragma unroll
-    for (int t = 0; t < DB; ++t) st.acc[t] = mfma32(pa, vf[t], st.acc[t]);
-    st.m = mn;  // kernel.py:172
-}
-
-// Output codes of the wave's 32 rows (kernel.py:176-180):
-// out = int8(cvt_x86(RN_f32(fp32(acc) / fp32(l)))).
-// The quotient is taken as RN_f32(a * y) in double precision, y = RN_f64(1/b)
-// once per row.  a * y is within 2^-52 (relative) of a/b, while a/b, for
-// 24-bit a and b, is never within 2^-49 of a midpoint between two floats (it
-// cannot be one: that would need a 25-bit odd significand), so rounding the
-// double to float gives exactly the IEEE single division.  For |b| >= 2 the
-// quotient is below 2^30 in magnitude, so v_cvt_i32_f32 truncates exactly as
-// x86 does; a wave with any row of l in {-1, 0, 1} (quotient +-inf, NaN or
-// 2^31: INT_MIN on x86) takes the IEEE division and the x86 conversion.
-// Bytes go out with buffer stores: rows >= N fall beyond the buffer's range
-// ((N-1)*so2 + D bytes from the head's base, so2 >= D checked by the host)
-// and are dropped by the hardware.
-template <int D>
-__device__ __forceinline__ void fast_store(const FastState<D>& st, const Args& a, int z, int h, int lane, int q0,
-                                           double* yslot) {
-    constexpr int DB = D / 32;
-    const int lq = lane & 31, g = lane >> 5;
-    const float b_row = (float)st.l;            // S layout: lane = row
-    const double y_row = 1.0 / (double)b_row;
-    const bool exact = __any(st.l >= -1 && st.l <= 1);
-    // y of the 32 rows to LDS (this wave's 256 bytes), read back two rows at a
-    // time in the O layout (rows 8(v>>2) + 4g + (v&3), v and v+1 adjacent):
-    // 8 broadcast reads instead of 32 lane permutes
-    if (!exact && g == 0) yslot[lq] = y_row;
-    const int32_t so2 = (int32_t)a.so[2];
-    const __amdgpu_buffer_rsrc_t rsrc = out_rsrc(a, z, h, D);
-    const float os = a.out_dt == QFLASH_HIP_I8 ? 0.f : scale_value(a);
-    const int32_t voff = (q0 + 4 * g) * so2 + lq;
-    with_out_type(a.out_dt, [&]<int OUT>() {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int row = crow(v, lane);
-            const int32_t soff = (8 * (v >> 2) + (v & 3)) * so2;
-            if (!exact) {
-                const double yd = yslot[row];
-#pragma unroll
-                for (int t = 0; t < DB; ++t) {
-                    const float qf = (float)((double)(float)st.acc[t][v] * yd);
-                    put_out<OUT>(rsrc, (int32_t)qf, voff + t * 32, soff, os);
-                }
-            } else {
-                const float bf = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * row, __float_as_int(b_row)));
-#pragma unroll
-                for (int t = 0; t < DB; ++t) {
-                    const int32_t code = cvt_x86(__fdiv_rn((float)st.acc[t][v], bf));
-                    put_out<OUT>(rsrc, code, voff + t * 32, soff, os);
-                }
-            }
-        }
-    });
-}
-
-// The 32 query rows of one wave: K / V stages double-buffered in LDS (the
-// copy of stage s+1 runs while stage s is consumed), full 32-key steps in the
-// loop, a final partial step (N % 32 != 0) after it from the last stage's
-// buffer, which no later copy overwrites, then the rows' int8 codes.  Every
-// wave of the workgroup issues its share of the copies and passes the same
-// barriers, active or not.
-template <int D, int W, bool MASKED, bool WIDE, bool DYN>
-__device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t* smem, const int8_t* kb,
-                                          const int8_t* vb, int z, int h, const BiasRow& brow, int wave, int lane,
-                                          int q0, bool active, bool wave_fast, int32_t xlim, int lut_mode) {
-    using S = Stage<D, W>;
-    constexpr int DB = D / 32;
-    constexpr int LUT = 2 * S::BYTES;  // LDS address of the p table (smem starts at 0)
-    FastState<D> st;
-#pragma unroll
-    for (int t = 0; t < DB; ++t) st.acc[t] = i32x16{};
-    st.m = kNegInf + (MASKED ? 0 : kScoreBias);  // kernel.py:138
-    st.l = 1;                                     // kernel.py:139
-    st.bnd = 0.f;
-    st.wide = 0;
-    // all bytes -128; opaque to the compiler each step, so that the bias MFMA
-    // is issued per step rather than hoisted into 16 live registers
-    i32x4 xb = i32x4{(int32_t)0x80808080, (int32_t)0x80808080, (int32_t)0x80808080, (int32_t)0x80808080};
-
-    // K / V of this head as buffers ending after row N-1: rows >= N read as 0
-    const __amdgpu_buffer_rsrc_t rk =
-        __builtin_amdgcn_make_buffer_rsrc((void*)kb, 0, (a.N - 1) * (int32_t)a.sk[2] + D, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rv =
-        __builtin_amdgcn_make_buffer_rsrc((void*)vb, 0, (a.N - 1) * (int32_t)a.sv[2] + D, 0x00020000);
-    const StageDma<D, W> dma(a, wave, lane);
-    const Frag<D> fr(lane);
-    dma.issue(rk, rv, smem, 0, a, wave);
-    stage_sync();
-
-    static_assert(S::BYTES >= W * 256, "epilogue slots of 256 bytes per wave in one stage buffer");
-    const int nfull = a.N >> 5;
-    const int nstage = (a.N + S::KEYS - 1) / S::KEYS;
-    // step 0 (m = NEG_INF, acc = 0) apart from the loop: the loop body then
-    // carries no first-step cases
-    if (active && nfull > 0)
-        fast_step<D, LUT, MASKED, false, WIDE, DYN, true>(st, a, qv, smem, smem + S::KBYTES, fr, brow, 0, lane,
-                                                          wave_fast, xlim, lut_mode, xb);
-    for (int stg = 0; stg < nstage; ++stg) {
-        const int8_t* buf = smem + (stg & 1) * S::BYTES;
-        if (stg + 1 < nstage) dma.issue(rk, rv, smem + ((stg + 1) & 1) * S::BYTES, (stg + 1) * S::KEYS, a, wave);
-        if (active) {
-            // unrolled: the steps' LDS offsets within the stage are immediates
-#pragma unroll
-            for (int half = 0; half < S::STEPS; ++half) {
-                const int step = stg * S::STEPS + half;
-                if (half == 0 && stg == 0) continue;  // step 0 ran above
-                if (step >= nfull) break;
-                if constexpr (!MASKED) asm volatile("" : "+v"(xb));
-                fast_step<D, LUT, MASKED, false, WIDE, DYN, false>(st, a, qv, buf + half * 32 * D,
-                                                                   buf + S::KBYTES + half * 32 * D, fr, brow,
-                                                                   step * 32, lane, wave_fast, xlim, lut_mode, xb);
-            }
-        }
-        stage_sync();
-    }
-    if (active && (a.N & 31)) {
-        const int8_t* buf = smem + ((nstage - 1) & 1) * S::BYTES;
-        const int th = nfull % S::STEPS;
-        const int8_t* lk = buf + th * 32 * D;
-        const int8_t* lv = buf + S::KBYTES + th * 32 * D;
-        if (nfull == 0)
-            fast_step<D, LUT, MASKED, true, WIDE, DYN, true>(st, a, qv, lk, lv, fr, brow, 0, lane, wave_fast, xlim,
-                                                             lut_mode, xb);
-        else if ((a.N & 31) <= 8)  // keys of the first TV score registers only
-            fast_step<D, LUT, MASKED, true, WIDE, DYN, false, 4>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane,
-                                                                 wave_fast, xlim, lut_mode, xb);
-        else if ((a.N & 31) <= 16)
-            fast_step<D, LUT, MASKED, true, WIDE, DYN, false, 8>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane,
-                                                                 wave_fast, xlim, lut_mode, xb);
-        else if ((a.N & 31) <= 24)
-            fast_step<D, LUT, MASKED, true, WIDE, DYN, false, 12>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane,
-                                                                  wave_fast, xlim, lut_mode, xb);
-        else
-            fast_step<D, LUT, MASKED, true, WIDE, DYN, false>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane,
-                                                              wave_fast, xlim, lut_mode, xb);
-    }
-    if (!active) return;
-    // this wave's 256 bytes of the stage buffer that no step reads any more:
-    // the last stage used buffer (nstage - 1) & 1 and every wave has passed the
-    // barrier after the stage before it
-    fast_store<D>(st, a, z, h, lane, q0,
-                  reinterpret_cast<double*>(smem + (nstage & 1) * S::BYTES + wave * 256));
-}
-
-// Occupancy target (waves per SIMD) by head dim: the register budget of the
-// O accumulators (D/32 x 16 VGPRs) and the score / exp temporaries.  D = 32
-// fits 6 (80 VGPRs, no spills; measured 5 % faster than 4 on Swin windows,
-// 8 slower).
-template <int D>
-constexpr int fast_waves_per_simd() { return D <= 32 ? 6 : (D == 64 ? QF_FAST_WAVES_D64 : 2); }
-
-template <int D, int W, bool MASKED, bool DYN>
-__global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Args a) {
-    using S = Stage<D, W>;
-    constexpr int DB = D / 32;
-    __shared__ __attribute__((aligned(16))) int8_t smem[2 * S::BYTES + kLutMax];
-
-    const int tid = threadIdx.x;
-    // p(u) table, entry lut_n - 1 - u (lut_pack_vt), visible after fast_rows'
-    // first barrier; lut_n - 1 <= x_safe (host), where the 24-bit E is exact
-    for (int u = tid; u < a.lut_n; u += 64 * W)
-        smem[2 * S::BYTES + a.lut_n - 1 - u] =
-            (int8_t)(mad24(exp2_fast(-u, a.eM, a.rs), a.rM, 1 << 15) >> 16);
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-    const int lq = lane & 31, g = lane >> 5;
-    const int wg = xcd_order(blockIdx.x, a.n_wg);
-    const int zh = wg / a.mblocks, mb = wg % a.mblocks;
-    const int z = zh / a.H, h = zh % a.H;
-    const int q0 = (mb * W + wave) * 32;
-    const bool active = q0 < a.N;
-    const int qrow = q0 + lq;
-
-    const int8_t* qb = a.q + z * a.sq[0] + h * a.sq[1];
-    const int8_t* kb = a.k + z * a.sk[0] + h * a.sk[1];
-    const int8_t* vb = a.v + z * a.sv[0] + h * a.sv[1];
-    BiasRow brow;
-    if constexpr (MASKED) {
-        const int32_t* bh = a.bias + (a.bias_zmod ? z % a.bias_zmod : z) * a.sb[0] + h * a.sb[1];
-        brow.row = qrow < a.N ? bh + (int64_t)qrow * a.sb[2] : nullptr;
-        // extent of this head's bias: the last element of row N-1 (strides >= 0 when bias_vec)
-        const int32_t nbytes = a.bias_vec ? (int32_t)(((a.N - 1) * a.sb[2] + a.N) * 4) : 0;
-        brow.rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)bh, 0, nbytes, 0x00020000);
-        brow.voff = (int32_t)((qrow * a.sb[2] + 4 * g) * 4);
-    } else {
-        brow.row = nullptr;
-        brow.voff = 0;
-        brow.rsrc = __builtin_amdgcn_make_buffer_rsrc(nullptr, 0, 0, 0x00020000);
-    }
-
-    i32x4 qv[DB];
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-        qv[db] = qrow < a.N ? *reinterpret_cast<const i32x4*>(qb + (int64_t)qrow * a.sq[2] + db * 32 + g * 16)
-                            : i32x4{0, 0, 0, 0};
-
-    // Unmasked: every real key column of this row has |s| <= 128*||q_row||_1, so
-    // |x| = |s - m'| <= X_row for the scores and, past the first step, for
-    // m - m'; the 24-bit path is exact when X_row*|eM| and the |a| bound stay in
-    // range (checked once for the whole wave).  Masked: |x| <= x_safe is checked
-    // per step.
-    bool wave_fast = !a.force_robust;
-    int32_t xlim = a.x_safe;
-    // the table sits at LDS address 2 * S::BYTES, the byte loads' immediate offset
-    const bool lut_at = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t*)smem == 0;
-    int lut_mode = a.lut_n && lut_at ? 2 : 0;  // 1: u <= lut_lim for every real column, 2: checked per step
-    if constexpr (!MASKED) {
-        // sum |q|: bytes offset by 128 (xor 0x80) against 0x80 under v_sad_u8
-        uint32_t l1u = 0;
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-            for (int w4 = 0; w4 < 4; ++w4)
-                l1u = __builtin_amdgcn_sad_u8((uint32_t)qv[db][w4] ^ 0x80808080u, 0x80808080u, l1u);
-        const int32_t l1 = half_sum((int32_t)l1u);
-        // real columns: x = s - m' >= -2*smax (padded columns are evaluated exactly apart)
-        const int64_t X = 2 * 128ll * l1;
-        const int64_t lim = (1ll << 31) - (1ll << 17);
-        const bool ok = X * (int64_t)(-(int64_t)a.eM) <= lim &&
-                        ((X * a.eps_abs + 65535) >> 16) + 2 * (int64_t)a.rs + 1 < (1 << 22);
-        wave_fast = wave_fast && __all(ok);
-        xlim = (int32_t)(X < (1 << 30) ? X : (1 << 30));
-        // biased scores >= kScoreBias - 128 * ||q||_1 > lut_n - 1: scores and thresholds positive
-        if (lut_mode) lut_mode = !__all(X / 2 + kLutMax <= kScoreBias) ? 0 : (__all(X <= a.lut_lim) ? 1 : 2);
-    }
-
-    // Unmasked waves whose guard holds run a loop that never meets an alpha
-    // outside [-1, rs] after the first step; the others (and masked waves) run
-    // the loop that also handles it.  Both pass the same barriers, and each
-    // writes its own rows, so the two never merge register state.
-    if constexpr (!MASKED) {
-        if (wave_fast)
-            fast_rows<D, W, false, false, DYN>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active, wave_fast, xlim,
-                                               lut_mode);
-        else
-            fast_rows<D, W, false, true, DYN>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active, wave_fast, xlim,
-                                               lut_mode);
-    } else {
-        fast_rows<D, W, true, true, DYN>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active, wave_fast, xlim,
-                                               lut_mode);
-    }
-}
 
 __global__ __launch_bounds__(64) void mfma_layout_kernel(const int8_t* A, const int8_t* B, int32_t* C) {
     const int lane = threadIdx.x, lq = lane & 31, g = lane >> 5;
@@ -1353,89 +40,33 @@ __global__ __launch_bounds__(64) void mfma_layout_kernel(const int8_t* A, const 
 using qferr::fail;
 using qferr::g_err;
 
-// ---- occupancy ------------------------------------------------------------
-// The fast kernel runs at its natural occupancy (as many workgroups per CU as
-// its registers allow): measured on MI355X, 4 waves per SIMD beat 3 even where
-// 3 would split the grid into whole rounds (cfg3: 142 us vs 198 us).  The
-// tuning hook QFLASH_HIP_WG_PER_CU lowers it by padding the workgroup's LDS
-// allocation (dynamic shared memory the kernel does not use).
-
-static int device_attr(hipDeviceAttribute_t attr) {
-    int dev = 0, v = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, attr, dev) != hipSuccess) return 0;
-    return v;
+// ---- test and tuning hooks --------------------------------------------------
+// Read from the environment once, when the library is loaded, never per
+// launch: the test-hook bits (QFLASH_HIP_FORCE_GENERAL, _FORCE_DYNAMIC_BOUND,
+// _FORCE_ROBUST, _NO_LUT, _FORCE_LUT set to a non-zero value) and two tuning
+// values (QFLASH_HIP_WG_PER_CU: workgroups per CU of the fast kernel, 0 = its
+// natural occupancy; QFLASH_HIP_WAVES_PER_WG: 1, 2 or 4).  Tests change the
+// bits through qflash_hip_set_test_hooks; launches read them with one relaxed
+// atomic load.
+static bool env_flag(const char* name) {
+    const char* v = getenv(name);
+    return v && v[0] && v[0] != '0';
 }
-
-static int pick_wg_per_cu(int kmax) {
-    const char* env = getenv("QFLASH_HIP_WG_PER_CU");  // tuning hook
-    if (env && atoi(env) > 0) return atoi(env) < kmax ? atoi(env) : kmax;
-    return kmax;
+static int env_int(const char* name) {
+    const char* v = getenv(name);
+    return v ? atoi(v) : 0;
 }
-
-// Dynamic LDS bytes that limit `kern` to k workgroups per CU (cached per k).
-template <typename Kern>
-static size_t lds_pad_for(Kern kern, int block, int k, std::atomic<int>* cache) {
-    int c = cache[k].load(std::memory_order_relaxed);
-    if (c >= 0) return (size_t)c;
-    const int lds_cu = device_attr(hipDeviceAttributeMaxSharedMemoryPerMultiprocessor);
-    hipFuncAttributes fa;
-    int pad = 0;
-    if (lds_cu > 0 && hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(kern)) == hipSuccess) {
-        const int want = (lds_cu / k) & ~511;
-        pad = want > (int)fa.sharedSizeBytes ? want - (int)fa.sharedSizeBytes : 0;
-        if (pad > 48 * 1024) pad = 0;
-        int n = 0;
-        if (pad && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(kern), block,
-                                                                 (size_t)pad) != hipSuccess || n != k))
-            pad = 0;
-    }
-    cache[k].store(pad, std::memory_order_relaxed);
-    return (size_t)pad;
+static uint32_t env_hook_bits() {
+    return (env_flag("QFLASH_HIP_FORCE_GENERAL") ? QFLASH_HIP_HOOK_FORCE_GENERAL : 0u) |
+           (env_flag("QFLASH_HIP_FORCE_DYNAMIC_BOUND") ? QFLASH_HIP_HOOK_FORCE_DYNAMIC_BOUND : 0u) |
+           (env_flag("QFLASH_HIP_FORCE_ROBUST") ? QFLASH_HIP_HOOK_FORCE_ROBUST : 0u) |
+           (env_flag("QFLASH_HIP_NO_LUT") ? QFLASH_HIP_HOOK_NO_LUT : 0u) |
+           (env_flag("QFLASH_HIP_FORCE_LUT") ? QFLASH_HIP_HOOK_FORCE_LUT : 0u);
 }
-
-template <int D, int W, bool MASKED, bool DYN>
-static hipError_t launch_fast(const Args& a, dim3 grid, hipStream_t st) {
-    static std::atomic<int> kmax_cache{0};
-    static std::atomic<int> pad_cache[9] = {-1, -1, -1, -1, -1, -1, -1, -1, -1};
-    auto kern = fwd_fast<D, W, MASKED, DYN>;
-    int kmax = kmax_cache.load(std::memory_order_relaxed);
-    if (kmax <= 0) {
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&kmax, reinterpret_cast<const void*>(kern), 64 * W, 0) !=
-            hipSuccess)
-            kmax = 1;
-        kmax = kmax < 1 ? 1 : (kmax > 8 ? 8 : kmax);
-        kmax_cache.store(kmax, std::memory_order_relaxed);
-    }
-    const int k = pick_wg_per_cu(kmax);
-    const size_t pad = k < kmax ? lds_pad_for(kern, 64 * W, k, pad_cache) : 0;
-    hipLaunchKernelGGL(kern, grid, dim3(64 * W), pad, st, a);
-    return hipGetLastError();
-}
-
-template <int D, int W, bool MASKED>
-static hipError_t launch_dw(const Args& a, bool vec, bool fast, dim3 grid, hipStream_t st) {
-    if constexpr (D <= 128) {
-        // DYN: the identity of the rescale by alpha = rs is proved per row in-kernel
-        if (fast) return a.id_ok ? launch_fast<D, W, MASKED, false>(a, grid, st)
-                                 : launch_fast<D, W, MASKED, true>(a, grid, st);
-    }
-    if (vec)
-        hipLaunchKernelGGL((fwd_general<D, W, MASKED, true>), grid, dim3(64 * W), 0, st, a);
-    else
-        hipLaunchKernelGGL((fwd_general<D, W, MASKED, false>), grid, dim3(64 * W), 0, st, a);
-    return hipGetLastError();
-}
-
-template <int D, bool MASKED>
-static hipError_t launch_d(const Args& a, int W, bool vec, bool fast, dim3 grid, hipStream_t st) {
-    switch (W) {
-        case 1: return launch_dw<D, 1, MASKED>(a, vec, fast, grid, st);
-        case 2: return launch_dw<D, 2, MASKED>(a, vec, fast, grid, st);
-        default: return launch_dw<D, 4, MASKED>(a, vec, fast, grid, st);
-    }
-}
-
-static bool getenv_flag(const char* name);
+static std::atomic<uint32_t> g_hook_bits{env_hook_bits()};
+static const int g_wg_per_cu = env_int("QFLASH_HIP_WG_PER_CU");
+static const int g_waves_per_wg = env_int("QFLASH_HIP_WAVES_PER_WG");
+static bool hook(uint32_t bit) { return (g_hook_bits.load(std::memory_order_relaxed) & bit) != 0; }
 
 // Bounds of the fast kernel's exp2 + requantisation table (see lut_pack_vt):
 // n entries p(0 .. n - 1), the last one 0, and lim such that p(u) = 0 for
@@ -1473,11 +104,11 @@ static void lut_bounds(const Args& a, int32_t* n_out, int32_t* lim_out) {
 static void choose_lut(Args& a, int W) {
     a.lut_n = 0;
     a.lut_lim = 0;
-    if (a.force_robust || getenv_flag("QFLASH_HIP_NO_LUT")) return;  // test hooks
+    if (a.force_robust || hook(QFLASH_HIP_HOOK_NO_LUT)) return;  // test hooks
     // the table replaces ~80 VALU instructions per 32-key step, and filling it
     // costs each wave ~10 per 64 * W entries
     const bool pays = a.N >= 32;
-    if (!pays && !getenv_flag("QFLASH_HIP_FORCE_LUT")) return;
+    if (!pays && !hook(QFLASH_HIP_HOOK_FORCE_LUT)) return;
     int32_t n, lim;
     lut_bounds(a, &n, &lim);
     if (n - 1 > a.x_safe) return;  // the kernel fills the table with the 24-bit E
@@ -1526,11 +157,6 @@ static bool choose_fast(Args& a, int D, bool masked, bool vec) {
 }
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
-
-static bool getenv_flag(const char* name) {
-    const char* v = getenv(name);
-    return v && v[0] && v[0] != '0';
-}
 
 static int forward(const int8_t* Q, const int8_t* K, const int8_t* V, void* O, const int32_t* bias,
                    int32_t rs, int32_t eM, int32_t rM, int32_t lM, int32_t aM, const int64_t* strides,
@@ -1591,8 +217,7 @@ static int forward(const int8_t* Q, const int8_t* K, const int8_t* V, void* O, c
 
     const int blocks32 = (N + 31) / 32;
     int W = blocks32 >= 4 ? 4 : (blocks32 >= 2 ? 2 : 1);
-    if (const char* ew = getenv("QFLASH_HIP_WAVES_PER_WG"))  // tuning hook: 1, 2 or 4
-        if (atoi(ew) == 1 || atoi(ew) == 2 || atoi(ew) == 4) W = atoi(ew);
+    if (g_waves_per_wg == 1 || g_waves_per_wg == 2 || g_waves_per_wg == 4) W = g_waves_per_wg;  // tuning hook
     a.mblocks = (blocks32 + W - 1) / W;
     const int64_t nwg = (int64_t)Z * H * a.mblocks;
     if (nwg > INT32_MAX) return fail(QFLASH_HIP_EINVAL, "grid too large");
@@ -1602,30 +227,29 @@ static int forward(const int8_t* Q, const int8_t* K, const int8_t* V, void* O, c
     a.x_safe = 0;
     a.eps_abs = 0;
     a.e_acc = 0;
-    // Test hooks (environment, read per call): QFLASH_HIP_FORCE_GENERAL selects the
-    // general kernel; QFLASH_HIP_FORCE_DYNAMIC_BOUND / QFLASH_HIP_FORCE_ROBUST drive the
-    // fast kernel's exact fallbacks on inputs that would not need them.
-    // QFLASH_HIP_NO_LUT / QFLASH_HIP_FORCE_LUT turn the fast kernel's table path
-    // off / on whatever the shape.
-    a.force_robust = getenv_flag("QFLASH_HIP_FORCE_ROBUST") ? 1 : 0;
-    const bool fast = choose_fast(a, D, masked, vec) && !getenv_flag("QFLASH_HIP_FORCE_GENERAL");
+    // Test hooks: FORCE_GENERAL selects the general kernel; FORCE_DYNAMIC_BOUND /
+    // FORCE_ROBUST drive the fast kernel's exact fallbacks on inputs that would
+    // not need them; NO_LUT / FORCE_LUT turn its table path off / on whatever
+    // the shape.
+    a.force_robust = hook(QFLASH_HIP_HOOK_FORCE_ROBUST) ? 1 : 0;
+    const bool fast = choose_fast(a, D, masked, vec) && !hook(QFLASH_HIP_HOOK_FORCE_GENERAL);
     if (fast) choose_lut(a, W);
-    if (getenv_flag("QFLASH_HIP_FORCE_DYNAMIC_BOUND")) a.id_ok = 0;
+    if (hook(QFLASH_HIP_HOOK_FORCE_DYNAMIC_BOUND)) a.id_ok = 0;
     dim3 grid((unsigned)nwg);
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;
 #define QF_CASE(DD)                                                                      \
     case DD:                                                                             \
-        e = masked ? launch_d<DD, true>(a, W, vec, fast, grid, st)                       \
-                   : launch_d<DD, false>(a, W, vec, fast, grid, st);                     \
+        e = masked ? launch_d<DD, true>(a, W, vec, fast, g_wg_per_cu, grid, st)          \
+                   : launch_d<DD, false>(a, W, vec, fast, g_wg_per_cu, grid, st);        \
         break;
     switch (D) {
         QF_CASE(32)
         QF_CASE(64)
         QF_CASE(128)
         default:
-            e = masked ? launch_d<256, true>(a, W, vec, fast, grid, st)
-                       : launch_d<256, false>(a, W, vec, fast, grid, st);
+            e = masked ? launch_d<256, true>(a, W, vec, fast, g_wg_per_cu, grid, st)
+                       : launch_d<256, false>(a, W, vec, fast, g_wg_per_cu, grid, st);
     }
 #undef QF_CASE
     if (e != hipSuccess) return fail(QFLASH_HIP_ELAUNCH, "launch failed: %s", hipGetErrorString(e));
@@ -1695,6 +319,10 @@ int qflash_hip_lut_bounds(int32_t sm_rscale, int32_t exp_M, int32_t req_M, int32
     return QFLASH_HIP_OK;
 }
 
-const char* qflash_hip_version(void) { return "qflash_hip 0.1 (gfx950)"; }
+uint32_t qflash_hip_set_test_hooks(uint32_t bits) {
+    return qf::g_hook_bits.exchange(bits & QFLASH_HIP_HOOK_ALL, std::memory_order_relaxed);
+}
+
+const char* qflash_hip_version(void) { return "qflash_hip 0.2 (gfx950)"; }
 
 }  // extern "C"

@@ -25,3 +25,20 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+@pytest.fixture
+def hip_hooks():
+    """Set the HIP library's test hooks for one test: hip_hooks("FORCE_LUT", ...);
+    the previous bits come back at teardown."""
+    from qflash_amd import _lib
+
+    prev = []
+
+    def set_(*names):
+        old = _lib.set_test_hooks(*names)
+        if not prev:
+            prev.append(old)
+    yield set_
+    if prev:
+        _lib.load().qflash_hip_set_test_hooks(prev[0])

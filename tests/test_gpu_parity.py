@@ -76,19 +76,18 @@ def test_golden_codes(name):
     np.testing.assert_array_equal(o.cpu().numpy(), c["o_i8"])
 
 
-HOOKS = ["QFLASH_HIP_FORCE_GENERAL", "QFLASH_HIP_FORCE_DYNAMIC_BOUND", "QFLASH_HIP_FORCE_ROBUST", "QFLASH_HIP_NO_LUT",
-         "QFLASH_HIP_FORCE_LUT"]
+HOOKS = ["FORCE_GENERAL", "FORCE_DYNAMIC_BOUND", "FORCE_ROBUST", "NO_LUT", "FORCE_LUT"]
 
 
 @pytest.mark.parametrize("hook", HOOKS)
 @pytest.mark.parametrize("name", sorted(CASES))
-def test_golden_codes_forced_paths(name, hook, monkeypatch):
+def test_golden_codes_forced_paths(name, hook, hip_hooks):
     """Every exact fallback on every case: the general kernel (used when the fast
     path's constant guards fail), the fast kernel's per-row dynamic bound for the
     identity rescale, its robust continuation (general arithmetic, used when a
     per-wave or per-step guard fails), and its arithmetic and table exp2 paths
     (the table off / on whatever the launch size)."""
-    monkeypatch.setenv(hook, "1")
+    hip_hooks(hook)
     test_golden_codes(name)
 
 
@@ -149,8 +148,8 @@ CONFIG_SEEDS = [(c, s) for c in ("cfg1", "cfg2", "cfg3", "cfg4") for s in (0, 1,
 
 @pytest.mark.parametrize("hook", HOOKS[1:])
 @pytest.mark.parametrize("cfg_name", ["cfg1", "cfg3", "cfg4"])
-def test_config_codes_forced_paths(cfg_name, hook, monkeypatch):
-    monkeypatch.setenv(hook, "1")
+def test_config_codes_forced_paths(cfg_name, hook, hip_hooks):
+    hip_hooks(hook)
     test_config_codes_vs_oracle(cfg_name, 1)
 
 
@@ -205,13 +204,13 @@ def test_adversarial_int8_inputs(pattern, D, sm_scale):
 @pytest.mark.parametrize("masked", [False, True])
 @pytest.mark.parametrize("D", [32, 64, 128])
 @pytest.mark.parametrize("sm_scale", [1 / 3.4, 1 / 2.6, 1 / 57.3, 1 / 94.2, 0.0123])
-def test_table_path_vs_oracle(sm_scale, D, masked, monkeypatch):
+def test_table_path_vs_oracle(sm_scale, D, masked, hip_hooks):
     """The exp2 table of the fast kernel under scales with both signs of
     kappa: with small zero ranges (1/3.4: lut_lim = 25) most steps fail the
     per-step check and mix with the arithmetic path; rows of growing spread
     reach every case."""
     import ctypes
-    monkeypatch.setenv("QFLASH_HIP_FORCE_LUT", "1")
+    hip_hooks("FORCE_LUT")
     from qflash_amd.kernel import fixed_point_constants, mask_to_bias
     consts = Consts(*fixed_point_constants(sm_scale, 30, 30))
     n, lim = ctypes.c_int32(), ctypes.c_int32()
@@ -237,7 +236,7 @@ def test_table_path_vs_oracle(sm_scale, D, masked, monkeypatch):
 
 
 @pytest.mark.parametrize("sm_scale", [0.05, 1 / 57.3])
-def test_table_path_at_score_bias_edge(sm_scale, monkeypatch):
+def test_table_path_at_score_bias_edge(sm_scale, hip_hooks):
     """The unmasked table path takes one saturating subtraction per score,
     which needs every biased score positive: a wave may use it only while
     128 * ||q_row||_1 + 4096 <= 2^19 (||q||_1 <= 4064).  Rows of wave 0 sit on
@@ -245,7 +244,7 @@ def test_table_path_at_score_bias_edge(sm_scale, monkeypatch):
     to 4096), rows of wave 1 one past it (4065: arithmetic path); the spread
     of the scores in a step stays small, so the steps do take the table."""
     import ctypes
-    monkeypatch.setenv("QFLASH_HIP_FORCE_LUT", "1")
+    hip_hooks("FORCE_LUT")
     from qflash_amd.kernel import fixed_point_constants
     consts = Consts(*fixed_point_constants(sm_scale, 30, 30))
     n, lim = ctypes.c_int32(), ctypes.c_int32()
@@ -269,23 +268,34 @@ def test_table_path_at_score_bias_edge(sm_scale, monkeypatch):
     assert int((o.cpu().numpy() != want).sum()) == 0
 
 
+TAIL_MODES = {  # hooks, score spread
+    "table": (("FORCE_LUT",), 4.0),     # every step on the table
+    "mixed": (("FORCE_LUT",), 40.0),    # wide spreads: some steps fail the per-step table check
+    "arith": (("NO_LUT",), 4.0),        # the 24-bit arithmetic exp2
+    "robust": (("FORCE_ROBUST",), 4.0),  # general arithmetic inside the fast kernel
+}
+
+
+@pytest.mark.parametrize("mode", sorted(TAIL_MODES))
 @pytest.mark.parametrize("masked", [False, True])
-@pytest.mark.parametrize("D", [32, 64])
-@pytest.mark.parametrize("N", [33, 36, 37, 40, 41, 48, 49, 56, 57, 68])
-def test_table_path_short_tails(N, D, masked, monkeypatch):
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("N", [33, 36, 37, 40, 41, 48, 49, 56, 57, 60, 63, 68, 95])
+def test_table_path_short_tails(N, D, masked, mode, hip_hooks):
     """Partial last steps of 1-5 keys (the upper lane half of the step has no
-    real column up to 4), 8/9, 16/17 and 24/25 keys (the edges of the kernel's
-    4-, 8-, 12- and 16-register last steps), on the table path, masked or
-    not: the padded columns read entry 0 and l gets their exact p; small
-    score spreads and a small bias keep every step on the table."""
-    monkeypatch.setenv("QFLASH_HIP_FORCE_LUT", "1")
+    real column up to 4), 8/9, 16/17, 24/25 and 28-31 keys (the edges of the
+    kernel's 4-, 8-, 12- and 16-register last steps), masked or not, for
+    every head dim of the fast kernel, on the table path (padded columns read
+    entry 0 and l gets their exact p), with spreads wide enough that some
+    steps leave the table, on the arithmetic path and on the robust path."""
+    hooks, spread = TAIL_MODES[mode]
+    hip_hooks(*hooks)
     from qflash_amd.kernel import fixed_point_constants
     consts = Consts(*fixed_point_constants(1 / 57.3, 30, 30))
-    print(f"[case] N={N} D={D} masked={masked}", flush=True)
+    print(f"[case] N={N} D={D} masked={masked} mode={mode}", flush=True)
     g = np.random.default_rng(N * 7 + D + masked)
     Z, H = 2, 3
-    q = np.clip(np.rint(g.standard_normal((Z, H, N, D)) * 4), -128, 127)
-    k = np.clip(np.rint(g.standard_normal((Z, H, N, D)) * 4), -128, 127)
+    q = np.clip(np.rint(g.standard_normal((Z, H, N, D)) * spread), -128, 127)
+    k = np.clip(np.rint(g.standard_normal((Z, H, N, D)) * spread), -128, 127)
     v = g.integers(-128, 128, (Z, H, N, D))
     q8, k8, v8 = (torch.from_numpy(x.astype(np.int8)) for x in (q, k, v))
     bias = None
@@ -300,7 +310,7 @@ def test_table_path_short_tails(N, D, masked, monkeypatch):
 
 
 @pytest.mark.parametrize("case", range(24))
-def test_random_shapes_vs_oracle(case, monkeypatch):
+def test_random_shapes_vs_oracle(case, hip_hooks):
     """Seeded random shapes, scales, code spreads and biases through every
     fast-kernel path (table or not, masked or not, partial steps), bit-exact
     against the C oracle."""
@@ -313,7 +323,7 @@ def test_random_shapes_vs_oracle(case, monkeypatch):
     spread = float(g.choice([2.0, 8.0, 30.0, 90.0]))
     masked = bool(case % 3 == 0)
     if case % 2:
-        monkeypatch.setenv("QFLASH_HIP_FORCE_LUT", "1")
+        hip_hooks("FORCE_LUT")
     consts = Consts(*fixed_point_constants(sm, 30, 30))
     print(f"[case] {case}: Z={Z} H={H} N={N} D={D} sm={sm:.4f} spread={spread} masked={masked} "
           f"force_lut={case % 2}", flush=True)

@@ -92,17 +92,16 @@ def test_fused_dequantisation_equals_codes_times_scale(dtype, masked):
         m = torch.rand(N, N, generator=g) > 0.2
         bias = mask_to_bias(m.to(DEV), 0.01, Z, H, N)
     flags = dict(EXP_USE_SHIFT=True, L_USE_SHIFT=True, ACC_USE_SHIFT=True, L_SHIFT=30, ACC_SHIFT=30)
+    from qflash_amd import _lib
     for general in (False, True):
-        import os
-        if general:
-            os.environ["QFLASH_HIP_FORCE_GENERAL"] = "1"
+        prev = _lib.set_test_hooks(*(("FORCE_GENERAL",) if general else ()))
         try:
             o8 = torch.empty_like(v8)
             launch_forward(q8, k8, v8, o8, consts, flags, bias)
             out = torch.empty_like(v8, dtype=dtype)
             launch_forward(q8, k8, v8, out, consts, flags, bias, o_scale=scales[2])
         finally:
-            os.environ.pop("QFLASH_HIP_FORCE_GENERAL", None)
+            _lib.load().qflash_hip_set_test_hooks(prev)
         torch.cuda.synchronize()
         want = o8 * scales[2]
         assert want.dtype == dtype and want.stride() == out.stride()
