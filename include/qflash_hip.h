@@ -111,6 +111,23 @@ int qflash_hip_scales(const void* q, const void* k, const void* v, int32_t dtype
                       void* scales, uint32_t* workspace, int64_t workspace_elems, void* stream);
 
 /*
+ * qflash_hip_scales without a workspace argument and without any allocation,
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  The partial maxima live in a static device
+ * array of QFLASH_HIP_SCALES_WORKSPACE uint32 entries (1 KiB per GPU, held
+ * until the process ends; its size does not depend on the inputs, so no input
+ * size is rejected beyond what qflash_hip_scales rejects).  Each call clears it
+ * with a fill kernel and then runs qflash_hip_scales on it.  All calls on one
+ * GPU share that array: calls that overlap in time on one GPU (different
+ * streams, different threads) race and must be serialised by the caller.
+ * `stream` must belong to the current device.  Same results as
+ * qflash_hip_scales.
+ */
+int qflash_hip_scales_noalloc(const void* q, const void* k, const void* v, int32_t dtype,
+                              const int64_t* shapes_strides, void* scales, void* stream);
+
+/*
  * int8 codes clamp(round(x / scale), -128, 127) of Q, K, V (qflash/kernel.py:
  * 309-311), scale = scales[0..2] as written by qflash_hip_scales (device
  * memory, read on the device: no host synchronisation).  The division is IEEE

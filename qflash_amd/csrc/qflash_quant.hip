@@ -25,6 +25,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/qflash_hip.h"
 #include "qf_common.h"
 
@@ -505,6 +507,33 @@ __global__ __launch_bounds__(256) void mask_bias_kernel(const float* mask, int64
     }
 }
 
+// ---- qflash_hip_scales_noalloc: the absmax workspace in static device memory.
+// One array per GPU (each device that loads the library holds its own copy,
+// kept until the process ends), found through hipGetSymbolAddress once per
+// device; host code uses only that address, never the array's name.
+__device__ __align__(256) uint32_t scratch[QFLASH_HIP_SCALES_WORKSPACE];
+constexpr int kMaxDevices = 64;
+static std::atomic<uint32_t*> g_scratch[kMaxDevices];
+
+__global__ __launch_bounds__(256) void clear_kernel(uint32_t* p, int n) {
+    for (int i = threadIdx.x; i < n; i += 256) p[i] = 0u;
+}
+
+// The device address of `scratch` on device `dev` (the current device), or
+// nullptr with the error message set.
+static uint32_t* scratch_ptr(int dev) {
+    uint32_t* p = g_scratch[dev].load(std::memory_order_acquire);
+    if (p) return p;
+    void* a = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&a, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !a) {
+        fail(QFLASH_HIP_ELAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+        return nullptr;
+    }
+    g_scratch[dev].store(static_cast<uint32_t*>(a), std::memory_order_release);
+    return static_cast<uint32_t*>(a);
+}
+
 static int esize_of(int32_t dtype) {
     return dtype == QFLASH_HIP_F32 ? 4 : (dtype == QFLASH_HIP_F16 || dtype == QFLASH_HIP_BF16 ? 2 : 0);
 }
@@ -535,6 +564,28 @@ int qflash_hip_scales(const void* q, const void* k, const void* v, int32_t dtype
         case QFLASH_HIP_F16: return qfq::scales_dt<QFLASH_HIP_F16>(g, scales, workspace, st);
         default: return qfq::scales_dt<QFLASH_HIP_BF16>(g, scales, workspace, st);
     }
+}
+
+int qflash_hip_scales_noalloc(const void* q, const void* k, const void* v, int32_t dtype,
+                              const int64_t* shapes_strides, void* scales, void* stream) {
+    qfq::g_err[0] = 0;
+    if (!q || !k || !v || !shapes_strides || !scales) return qfq::fail(QFLASH_HIP_EINVAL, "null pointer argument");
+    int dev = 0, sdev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return qfq::fail(QFLASH_HIP_ELAUNCH, "no current HIP device");
+    if (dev < 0 || dev >= qfq::kMaxDevices) return qfq::fail(QFLASH_HIP_EINVAL, "device %d out of range", dev);
+    // the static workspace of the stream's device is addressed from this one
+    if (stream && hipStreamGetDevice((hipStream_t)stream, &sdev) == hipSuccess && sdev != dev)
+        return qfq::fail(QFLASH_HIP_EINVAL, "stream belongs to device %d, current device is %d", sdev, dev);
+    uint32_t* ws = qfq::scratch_ptr(dev);
+    if (!ws) return QFLASH_HIP_ELAUNCH;
+    // every call starts from zeroed slots (a fill kernel, not a memset: the
+    // call may be captured into a graph), so a failed earlier call leaves
+    // nothing behind
+    hipLaunchKernelGGL(qfq::clear_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, ws,
+                       (int)QFLASH_HIP_SCALES_WORKSPACE);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess)
+        return qfq::fail(QFLASH_HIP_ELAUNCH, "launch failed: %s", hipGetErrorString(e));
+    return qflash_hip_scales(q, k, v, dtype, shapes_strides, scales, ws, QFLASH_HIP_SCALES_WORKSPACE, stream);
 }
 
 int qflash_hip_quantize(const void* q, const void* k, const void* v, int32_t dtype, const int64_t* shapes_strides,
