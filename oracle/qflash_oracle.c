@@ -37,7 +37,7 @@ static inline int32_t sra32(int32_t a, int32_t b) {
 }
 
 static inline int32_t tdiv32(int32_t a, int32_t b) {
-    /* C division truncates; INT32_MIN / -1 cannot occur (b = sm_rscale > 0) */
+    /* C division truncates; INT32_MIN / -1 (sm_rscale = -1) wraps to INT32_MIN as numpy's int32 does */
     return (int32_t)((int64_t)a / (int64_t)b);
 }
 
@@ -138,7 +138,7 @@ int qfo_attention_codes(const int8_t* q, const int8_t* k, const int8_t* v, int8_
                         const int64_t* st, int Z, int H, int N, int D, const qfo_params* p,
                         int n_threads, int zh_begin, int zh_end) {
     if (!q || !k || !v || !o || !st || !p || Z <= 0 || H <= 0 || N <= 0 || D <= 0) return -1;
-    if (p->sm_rscale <= 0) return -2;
+    if (p->sm_rscale == 0) return -2; /* the reference's host raises before any launch with rs = 0 */
     if (p->l_use_shift && (p->l_shift < 1 || p->l_shift > 62)) return -3;
     if (p->acc_use_shift && (p->acc_shift < 1 || p->acc_shift > 62)) return -3;
     if (zh_end <= 0 || zh_end > Z * H) zh_end = Z * H;

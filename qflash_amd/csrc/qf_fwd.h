@@ -152,9 +152,13 @@ __host__ __device__ __forceinline__ int32_t sra(int32_t a, int32_t b) {
     return (uint32_t)b > 31u ? (a >> 31) : (a >> b);
 }
 
+// `//` of two int32 values: truncating, and INT32_MIN // -1 wraps to INT32_MIN
+// (numpy's int32 arithmetic, which the Triton interpreter runs).
+__host__ __device__ __forceinline__ int32_t tdiv(int32_t a, int32_t b) { return (int32_t)((int64_t)a / b); }
+
 // exp2_i32: kernel.py:40-59.
 __host__ __device__ __forceinline__ int32_t exp2_i32(int32_t x, const Args& a) {
-    int32_t q = a.exp_mode ? (wmul(x, a.eM) >> 16) : (wsub(0, x) / a.rs);
+    int32_t q = a.exp_mode ? (wmul(x, a.eM) >> 16) : tdiv(wsub(0, x), a.rs);
     int32_t r = wadd(x, wmul(q, a.rs));
     return sra(wadd(r >> 1, a.rs), q);
 }
@@ -172,7 +176,7 @@ __device__ __forceinline__ int32_t release(int32_t x, int32_t alpha, int32_t M, 
         prod += 1ull << (shift - 1);
         return (int32_t)(uint32_t)(uint64_t)((int64_t)prod >> shift);
     }
-    return wmul(x, alpha) / rs;
+    return tdiv(wmul(x, alpha), rs);
 }
 
 // fp32 -> int32 as the reference's CPU path does it: truncate, INT_MIN for

@@ -173,7 +173,10 @@ static int forward(const int8_t* Q, const int8_t* K, const int8_t* V, void* O, c
                                          "(tl.static_assert(BLOCK_N <= HEAD_DIM))");
     if (D != 32 && D != 64 && D != 128 && D != 256)
         return fail(QFLASH_HIP_EHEADDIM, "HEAD_DIM=%d not in {32,64,128,256}", D);
-    if (rs <= 0) return fail(QFLASH_HIP_EINVAL, "sm_rscale must be positive (got %d)", rs);
+    // rs = round(1/sm_scale) is never 0 at the reference's launch (its host
+    // divides by it, kernel.py:306); a negative one (negative `scale`) runs the
+    // general kernel, exact for any constants
+    if (rs == 0) return fail(QFLASH_HIP_EINVAL, "sm_rscale must not be 0");
     qflash_hip_flags f = {1, 1, 1, 30, 30};
     if (flags) f = *flags;
     if (f.l_use_shift && (f.l_shift < 1 || f.l_shift > 62))

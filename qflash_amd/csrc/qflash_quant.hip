@@ -618,7 +618,7 @@ int qflash_hip_window_bias(const float* rel, const float* mask, int32_t n_win, i
     if (H <= 0 || N <= 0 || n_win <= 0 || (!mask && n_win != 1))
         return qfq::fail(QFLASH_HIP_EINVAL, "bad window bias shape nW=%d H=%d N=%d%s", n_win, H, N,
                          mask ? "" : " (no mask: nW must be 1)");
-    if (!(sm_scale > 0.0) || !(sm_scale < 1e30)) return qfq::fail(QFLASH_HIP_EINVAL, "bad sm_scale %g", sm_scale);
+    if (!(sm_scale != 0.0) || !(fabs(sm_scale) < 1e30)) return qfq::fail(QFLASH_HIP_EINVAL, "bad sm_scale %g", sm_scale);
     const int64_t nn = (int64_t)N * N, total = (int64_t)n_win * H * nn;
     if (total >= ((int64_t)1 << 31)) return qfq::fail(QFLASH_HIP_EINVAL, "window bias too large");
     // torch: x * LOG2E and x / sm_scale with host scalars, both taken to fp32
@@ -636,7 +636,7 @@ int qflash_hip_mask_bias(const float* mask, int64_t n, double sm_scale, int32_t*
     qfq::g_err[0] = 0;
     if (!mask || !out) return qfq::fail(QFLASH_HIP_EINVAL, "null pointer argument");
     if (n <= 0 || n >= ((int64_t)1 << 31)) return qfq::fail(QFLASH_HIP_EINVAL, "bad mask size %lld", (long long)n);
-    if (!(sm_scale > 0.0) || !(sm_scale < 1e30)) return qfq::fail(QFLASH_HIP_EINVAL, "bad sm_scale %g", sm_scale);
+    if (!(sm_scale != 0.0) || !(fabs(sm_scale) < 1e30)) return qfq::fail(QFLASH_HIP_EINVAL, "bad sm_scale %g", sm_scale);
     const float log2e = (float)1.44269504;
     const float inv_sm = 1.0f / (float)sm_scale;
     const bool vec = (((uintptr_t)mask | (uintptr_t)out) & 15u) == 0;

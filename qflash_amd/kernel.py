@@ -288,6 +288,15 @@ def _scales_workspace(device) -> Tensor:
     return ws
 
 
+def _drop_scales_workspace(device) -> None:
+    """Forget this thread's workspace after a failed call: a launch that failed
+    between the absmax pass and the pass that clears the slots would leave
+    stale maxima in it, so the next call starts from a fresh zeroed one."""
+    cache = getattr(_ws_cache, "d", None)
+    if cache is not None:
+        cache.pop((device.index, torch.cuda.current_stream(device).cuda_stream), None)
+
+
 def quantize_qkv(query: Tensor, key: Tensor, value: Tensor):
     """Per-tensor scales and int8 codes of Q, K, V on the device (kernel.py:294-311).
 
@@ -322,8 +331,11 @@ def quantize_qkv(query: Tensor, key: Tensor, value: Tensor):
     scales = torch.empty(4, dtype=T, device=query.device)
     stream = _stream_ptr(query)
     ptrs = [ctypes.c_void_p(x.data_ptr()) for x in (query, key, value)]
-    _lib.check(L.qflash_hip_scales(*ptrs, code, geo, ctypes.c_void_p(scales.data_ptr()),
-                                   ctypes.c_void_p(ws.data_ptr()), ws.numel(), stream), "qflash_hip_scales")
+    rc = L.qflash_hip_scales(*ptrs, code, geo, ctypes.c_void_p(scales.data_ptr()), ctypes.c_void_p(ws.data_ptr()),
+                             ws.numel(), stream)
+    if rc != 0:
+        _drop_scales_workspace(query.device)
+    _lib.check(rc, "qflash_hip_scales")
 
     def finish():
         q8, k8, v8 = (torch.empty_like(x, dtype=torch.int8) for x in (query, key, value))

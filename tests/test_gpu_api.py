@@ -196,3 +196,69 @@ def test_masked_kernel_strided_bias_columns():
     assert torch.equal(outs[0], outs[1])
     want = oracle_c.attention_codes(q8.cpu(), k8.cpu(), v8.cpu(), Consts(*consts), Flags(), bias=bias, threads=8)
     np.testing.assert_array_equal(outs[0].cpu().numpy(), want)
+
+
+def test_patch_attention_model_runs_the_kernels_bit_exactly(monkeypatch):
+    """patch_attention (qflash/attention.py:89-108) on a small model built from
+    timm-like stand-ins: every swapped module runs on the GPU and each
+    attention call returns the oracle's codes times o_scale for the inputs the
+    module handed over; the model output equals a second, unpatched run of the
+    same modules through the recorded outputs."""
+    from torch import nn
+
+    from qflash_amd import QAttention, QWindowAttention, patch_attention
+    from qflash_amd import attention as A
+    from test_api import TimmLikeAttention, TimmLikeWindowAttention
+
+    class Block(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.norm = nn.LayerNorm(192)
+            self.attn = TimmLikeAttention(192, 3)
+
+        def forward(self, x):
+            return x + self.attn(self.norm(x))
+
+    class WinStage(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.wattn = TimmLikeWindowAttention(96, 3, 7)
+
+        def forward(self, x, mask):
+            return x + self.wattn(x, mask)
+
+    class Model(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.blocks = nn.Sequential(Block(), Block())
+            self.win = WinStage()
+
+        def forward(self, x, xw, mask):
+            return self.blocks(x), self.win(xw, mask)
+
+    torch.manual_seed(4)
+    model = Model()
+    counts = patch_attention(model, attn_types=[TimmLikeAttention], window_attn_types=[TimmLikeWindowAttention])
+    assert counts == {"attn": 2, "wattn": 1}
+    assert isinstance(model.blocks[0].attn, QAttention) and isinstance(model.win.wattn, QWindowAttention)
+    model = model.to(DEV)
+    tap, wtap = _Tap(A.qflash.forward), _WindowTap(A.qflash_forward_window)
+    monkeypatch.setattr(A.qflash, "forward", tap)
+    monkeypatch.setattr(A, "qflash_forward_window", wtap)
+    x = torch.randn(2, 197, 192, device=DEV)
+    nW = 4
+    xw = torch.randn(2 * nW, 49, 96, device=DEV)
+    ys, xs = torch.meshgrid(torch.arange(7), torch.arange(7), indexing="ij")
+    region = (ys.flatten() >= 4).long() * 2 + (xs.flatten() >= 4).long()
+    mask = torch.zeros(nW, 49, 49)
+    mask[nW // 2:] = (region[:, None] != region[None, :]).float() * -100.0
+    with torch.no_grad():
+        y, yw = model(x, xw, mask.to(DEV))
+    torch.cuda.synchronize()
+    assert len(tap.calls) == 2 and len(wtap.calls) == 1
+    for q, k, v, m, out in tap.calls:
+        assert m is None
+        assert torch.equal(out.cpu(), _expected(q, k, v, None))
+    q, k, v, am, out = wtap.calls[0]
+    assert torch.equal(out.cpu(), _expected(q, k, v, am))
+    assert torch.isfinite(y).all() and torch.isfinite(yw).all()

@@ -343,3 +343,37 @@ def test_random_shapes_vs_oracle(case, hip_hooks):
     _launch(qd, kd, vd, o, consts, Flags(), None if bias is None else bias.to(DEV))
     torch.cuda.synchronize()
     assert int((o.cpu().numpy() != want).sum()) == 0
+
+
+@pytest.mark.parametrize("masked", [False, True])
+@pytest.mark.parametrize("scale", [-0.125, -1.0 / 57.3, -0.9])
+def test_negative_scale_vs_oracle(scale, masked):
+    """A negative `scale` argument (accepted by the reference: its constants come
+    out negative, kernel.py:300-307, and its kernels run on them) goes through
+    the general kernel, exact for any constants: codes equal the oracle's, and
+    qflash.forward returns them times o_scale."""
+    from qflash_amd import qflash
+    from qflash_amd.kernel import LOG2E, fixed_point_constants, mask_to_bias, quantize
+    g = torch.Generator().manual_seed(int(-scale * 1000) + masked)
+    Z, H, N, D = 2, 2, 77, 64
+    q, k, v = (torch.randn(Z, H, N, D, generator=g) for _ in range(3))
+    mask = None
+    if masked:
+        mask = torch.where(torch.rand(N, N, generator=g) < 0.2, -200.0, torch.randn(N, N, generator=g))
+    qs, ks, vs = (x.abs().amax() / 127 for x in (q, k, v))
+    sm = scale * LOG2E * (qs * ks).item()
+    consts = Consts(*fixed_point_constants(sm, 30, 30))
+    assert consts.sm_rscale < 0
+    q8, k8, v8 = quantize(q, qs), quantize(k, ks), quantize(v, vs)
+    bias = None if mask is None else mask_to_bias(mask, sm, Z, H, N, materialize=True)
+    print(f"[case] scale={scale} masked={masked} consts={consts}", flush=True)
+    want = oracle_c.attention_codes(q8, k8, v8, consts, Flags(), bias=bias, threads=8)
+    qd, kd, vd = q8.to(DEV), k8.to(DEV), v8.to(DEV)
+    o = torch.empty_like(vd)
+    _launch(qd, kd, vd, o, consts, Flags(), None if bias is None else bias.to(DEV))
+    torch.cuda.synchronize()
+    assert int((o.cpu().numpy() != want).sum()) == 0
+    out = qflash.forward(q.to(DEV), k.to(DEV), v.to(DEV), attn_mask=None if mask is None else mask.to(DEV),
+                         scale=scale)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), torch.from_numpy(want).float() * vs)

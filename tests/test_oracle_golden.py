@@ -194,3 +194,23 @@ def test_unmutated_loop_variant_is_the_oracle():
 def test_flags_dataclass_is_frozen():
     with pytest.raises(dataclasses.FrozenInstanceError):
         O.Flags().l_shift = 3
+
+
+@pytest.mark.parametrize("scale", [-0.125, -1.0 / 57.3, -0.9])
+def test_negative_scale_numpy_and_c_oracles_agree(scale):
+    """A negative `scale` gives negative constants (kernel.py:300-307), which the
+    reference's kernels take as they come; the numpy and C restatements agree on
+    them (masked and not), and the scalar loops agree on a small case."""
+    from qflash_amd.kernel import LOG2E, fixed_point_constants
+    g = np.random.default_rng(int(-scale * 1000))
+    Z, H, N, D = 1, 2, 45, 32
+    q, k, v = (g.integers(-128, 128, (Z, H, N, D)).astype(np.int8) for _ in range(3))
+    c = O.Consts(*fixed_point_constants(scale * LOG2E * 1e-3, 30, 30))
+    assert c.sm_rscale < 0
+    bias = g.integers(-3000, 3000, (Z, H, N, N)).astype(np.int32)
+    bias[g.random((Z, H, N, N)) < 0.2] = O.NEG_INF
+    for b in (None, bias):
+        want = O.attention_codes(q, k, v, c, O.Flags(), b)
+        np.testing.assert_array_equal(oracle_c.attention_codes(q, k, v, c, O.Flags(), b, threads=2), want)
+    small = O.attention_codes_scalar(q[:, :1, :12], k[:, :1, :12], v[:, :1, :12], c, O.Flags())
+    np.testing.assert_array_equal(small, O.attention_codes(q[:, :1, :12], k[:, :1, :12], v[:, :1, :12], c))
