@@ -585,15 +585,6 @@ __device__ __forceinline__ int32_t half_min(int32_t v) {
     const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
     return min((int32_t)r[0], (int32_t)r[1]);
 }
-// ds_bpermute_b32 with the lane's byte address split into a register and an
-// immediate offset: through the builtin the compiler hoists the 16 distinct
-// addresses of the rescale out of the loop and holds 16 VGPRs for them.
-template <int OFF>
-__device__ __forceinline__ int32_t bpermute_off(int32_t addr, int32_t v) {
-    int32_t r;
-    asm volatile("ds_bpermute_b32 %0, %1, %2 offset:%3\n\ts_waitcnt lgkmcnt(0)" : "=v"(r) : "v"(addr), "v"(v), "i"(OFF));
-    return r;
-}
 // Keeps the compiler from distributing a per-row constant back into the
 // per-element expressions (it would turn one mad into mul + sub + add).
 __device__ __forceinline__ int32_t opaque(int32_t v) {
@@ -1066,18 +1057,35 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
                                         1.0000010f, 1.f);
         if (chg) {
             // register pair v = rows rlo (lanes 0-31) and rlo+4 (lanes 32-63) of the O layout;
-            // the multiplier of row r sits in lane r of the S layout.
+            // the multiplier of row r sits in lane r of the S layout.  Two lane permutes
+            // (one LDS round trip for all pairs) lay the multipliers out as
+            //   m1: lane 16j + n holds row n + 4*(j >> 1),   m2: the same rows + 16,
+            // and a DPP row broadcast (row_newbcast:n, each 16-lane row takes its lane
+            // n) of m1 (rlo < 16) or m2 gives pair v's multipliers: row rlo in lanes
+            // 0-31, row rlo + 4 in lanes 32-63.
             // acc*A64 + 2^(as-1) mod 2^64 = acc*sext(A) + 2^(as-1) + (acc*Ah << 32)
             const int64_t ahalf = 1ll << (as - 1);
-            const int addr = g * 16;
+            const int src = 4 * ((lane & 15) + 4 * g);
+            const int32_t m1 = __builtin_amdgcn_ds_bpermute(src, A);
+            const int32_t m2 = __builtin_amdgcn_ds_bpermute(src + 64, A);
+            int32_t h1 = 0, h2 = 0;
+            if constexpr (WIDE)
+                if (wide) {
+                    h1 = __builtin_amdgcn_ds_bpermute(src, Ah);
+                    h2 = __builtin_amdgcn_ds_bpermute(src + 64, Ah);
+                }
             // bit rlo: row rlo or rlo + 4 changed (one scalar bit test per pair)
             const uint32_t pairs = (chg | (chg >> 4)) & 0x0F0F0F0Fu;
             auto pair = [&]<int V>() {
                 constexpr int rlo = 8 * (V >> 2) + (V & 3);
                 if ((pairs >> rlo) & 1u) {
-                    const int32_t av = bpermute_off<4 * rlo>(addr, A);
+                    const int32_t av = __builtin_amdgcn_update_dpp(0, rlo < 16 ? m1 : m2, 0x150 + (rlo & 15), 0xf,
+                                                                   0xf, false);
                     int32_t ah = 0;
-                    if constexpr (WIDE) ah = wide ? bpermute_off<4 * rlo>(addr, Ah) : 0;
+                    if constexpr (WIDE)
+                        ah = wide ? __builtin_amdgcn_update_dpp(0, rlo < 16 ? h1 : h2, 0x150 + (rlo & 15), 0xf, 0xf,
+                                                                false)
+                                  : 0;
 #pragma unroll
                     for (int t = 0; t < DB; ++t) {
                         const int64_t p = (int64_t)st.acc[t][V] * (int64_t)av + ahalf;
@@ -1257,22 +1265,15 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
 template <int D>
 constexpr int fast_waves_per_simd() { return D <= 32 ? 6 : (D == 64 ? QF_FAST_WAVES_D64 : 2); }
 
+// One workgroup of the single-tile kernel: row block mb (32 * W rows) of head
+// zh, in the LDS array smem whose table the caller has filled (visible after
+// fast_rows' first barrier).
 template <int D, int W, bool MASKED, bool DYN>
-__global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Args a) {
-    using S = Stage<D, W>;
+__device__ __forceinline__ void fast_block(const Args& a, int8_t* smem, int zh, int mb) {
     constexpr int DB = D / 32;
-    __shared__ __attribute__((aligned(16))) int8_t smem[2 * S::BYTES + kLutMax];
-
     const int tid = threadIdx.x;
-    // p(u) table, entry lut_n - 1 - u (lut_pack_vt), visible after fast_rows'
-    // first barrier; lut_n - 1 <= x_safe (host), where the 24-bit E is exact
-    for (int u = tid; u < a.lut_n; u += 64 * W)
-        smem[2 * S::BYTES + a.lut_n - 1 - u] =
-            (int8_t)(mad24(exp2_fast(-u, a.eM, a.rs), a.rM, 1 << 15) >> 16);
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int lq = lane & 31, g = lane >> 5;
-    const int wg = xcd_order(blockIdx.x, a.n_wg);
-    const int zh = wg / a.mblocks, mb = wg % a.mblocks;
     const int z = zh / a.H, h = zh % a.H;
     const int q0 = (mb * W + wave) * 32;
     const bool active = q0 < a.N;
@@ -1347,6 +1348,20 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
                                                lut_mode);
     }
 }
+
+template <int D, int W, bool MASKED, bool DYN>
+__global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Args a) {
+    using S = Stage<D, W>;
+    __shared__ __attribute__((aligned(16))) int8_t smem[2 * S::BYTES + kLutMax];
+    // p(u) table, entry lut_n - 1 - u (lut_pack_vt), visible after fast_rows'
+    // first barrier; lut_n - 1 <= x_safe (host), where the 24-bit E is exact
+    for (int u = threadIdx.x; u < a.lut_n; u += 64 * W)
+        smem[2 * S::BYTES + a.lut_n - 1 - u] =
+            (int8_t)(mad24(exp2_fast(-u, a.eM, a.rs), a.rM, 1 << 15) >> 16);
+    const int wg = xcd_order(blockIdx.x, a.n_wg);
+    fast_block<D, W, MASKED, DYN>(a, smem, wg / a.mblocks, wg % a.mblocks);
+}
+
 
 
 // ----------------------------------------------------------------------------
