@@ -1074,11 +1074,12 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
                     h1 = __builtin_amdgcn_ds_bpermute(src, Ah);
                     h2 = __builtin_amdgcn_ds_bpermute(src + 64, Ah);
                 }
-            // bit rlo: row rlo or rlo + 4 changed (one scalar bit test per pair)
+            // bit rlo: row rlo or rlo + 4 changed (one scalar bit test per pair; most
+            // are clear, so the pair's code is laid out off the fall-through path)
             const uint32_t pairs = (chg | (chg >> 4)) & 0x0F0F0F0Fu;
             auto pair = [&]<int V>() {
                 constexpr int rlo = 8 * (V >> 2) + (V & 3);
-                if ((pairs >> rlo) & 1u) {
+                if (__builtin_expect((pairs >> rlo) & 1u, 0)) {
                     const int32_t av = __builtin_amdgcn_update_dpp(0, rlo < 16 ? m1 : m2, 0x150 + (rlo & 15), 0xf,
                                                                    0xf, false);
                     int32_t ah = 0;
