@@ -162,6 +162,16 @@ int qflash_hip_window_bias(const float* rel, const float* mask, int32_t n_win, i
 int qflash_hip_mask_bias(const float* mask, int64_t n, double sm_scale, int32_t* out, void* stream);
 
 /*
+ * qflash_hip_window_bias / qflash_hip_mask_bias with sm_scale read from a
+ * device parameter block (qflash_hip_constants) instead of a host double, so
+ * that no host synchronisation precedes them; nothing is written when
+ * params[0] != 0.  No counterpart in the reference.
+ */
+int qflash_hip_window_bias_planned(const float* rel, const float* mask, int32_t n_win, int32_t H, int32_t N,
+                                   const int32_t* params, int32_t* out, void* stream);
+int qflash_hip_mask_bias_planned(const float* mask, int64_t n, const int32_t* params, int32_t* out, void* stream);
+
+/*
  * One entry point for every case of the forward, used by qflash_forward: the
  * masks of both masked entries (attn_bias NULL = unmasked; bias_zmod 0 = the
  * bias has Z slices, > 0 = window-periodic as in qflash_hip_window_kernel),
@@ -176,6 +186,44 @@ int qflash_hip_forward(const int8_t* Q, const int8_t* K, const int8_t* V, void* 
                        const void* o_scale, const int32_t* attn_bias, int32_t bias_zmod, int32_t sm_rscale,
                        int32_t exp_M, int32_t req_M, int32_t l_M, int32_t acc_M, const int64_t* strides, int32_t Z,
                        int32_t H, int32_t N_CTX, int32_t HEAD_DIM, const qflash_hip_flags* flags, void* stream);
+
+/*
+ * The five constants of qflash/kernel.py:297-307 formed on the device, so that
+ * a whole forward needs no host synchronisation (and can be captured in a HIP
+ * graph); no counterpart in the reference, which forms them on the host after
+ * `.item()`.  scales: the device array qflash_hip_scales writes (element 3 =
+ * q_scale * k_scale in `dtype`); scale: the host's (scale or 1/sqrt(D)) *
+ * 1.44269504 (kernel.py:289-290).  In Python's double arithmetic:
+ *   sm_scale = scale * double(scales[3]); sm_rscale = rint(1.0 / sm_scale);
+ *   exp_M = rint(-sm_scale * 65536); req_M = rint(sm_scale * 127 * 65536);
+ *   l_M = rint(2^l_shift / sm_rscale); acc_M = rint(2^acc_shift / sm_rscale)
+ * (rint = round half to even, Python's round).  params (device, 8-byte
+ * aligned, QFLASH_HIP_PARAMS_WORDS int32) receives: [0] a status, 0 or one of
+ * QFLASH_HIP_STATUS_* -- the first exception the reference's host raises on
+ * the same value, in its order of evaluation (then no attention kernel reads
+ * the constants and the outputs are left unwritten); [1..5] sm_rscale, exp_M,
+ * req_M, l_M, acc_M; [6..12] the fast kernel's plan for N_CTX, HEAD_DIM and
+ * masking; [14..15] sm_scale as a double.  Asynchronous on `stream`.
+ */
+#define QFLASH_HIP_PARAMS_WORDS 16
+#define QFLASH_HIP_STATUS_ZERODIV_SCALE 1   /* sm_scale == 0: ZeroDivisionError (1.0 / sm_scale) */
+#define QFLASH_HIP_STATUS_NAN 2             /* ValueError: cannot convert float NaN to integer */
+#define QFLASH_HIP_STATUS_INF 3             /* OverflowError: cannot convert float infinity to integer */
+#define QFLASH_HIP_STATUS_ZERODIV_RSCALE 4  /* sm_rscale == 0 (sm_scale > 2): ZeroDivisionError */
+#define QFLASH_HIP_STATUS_RANGE 5           /* a constant outside int32 (the kernels take int32) */
+int qflash_hip_constants(const void* scales, int32_t dtype, double scale, int32_t N_CTX, int32_t HEAD_DIM,
+                         int32_t masked, const qflash_hip_flags* flags, int32_t* params, void* stream);
+
+/*
+ * qflash_hip_forward with the constants in device memory (`params` from
+ * qflash_hip_constants with the same N_CTX, HEAD_DIM, masking and flags)
+ * instead of host integers.  No counterpart in the reference.  Nothing is
+ * written when params[0] != 0.
+ */
+int qflash_hip_forward_planned(const int8_t* Q, const int8_t* K, const int8_t* V, void* Out, int32_t out_dtype,
+                               const void* o_scale, const int32_t* attn_bias, int32_t bias_zmod,
+                               const int32_t* params, const int64_t* strides, int32_t Z, int32_t H, int32_t N_CTX,
+                               int32_t HEAD_DIM, const qflash_hip_flags* flags, void* stream);
 
 /* Message for the last failing call on this thread ("" if none). */
 const char* qflash_hip_last_error(void);

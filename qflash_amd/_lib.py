@@ -32,7 +32,8 @@ class Flags(ctypes.Structure):
 
 EXPORTS = ("qflash_hip_kernel", "qflash_hip_masked_kernel", "qflash_hip_window_kernel", "qflash_hip_forward",
            "qflash_hip_scales", "qflash_hip_scales_noalloc",
-           "qflash_hip_quantize", "qflash_hip_window_bias", "qflash_hip_mask_bias",
+           "qflash_hip_quantize", "qflash_hip_window_bias", "qflash_hip_mask_bias", "qflash_hip_constants",
+           "qflash_hip_forward_planned", "qflash_hip_window_bias_planned", "qflash_hip_mask_bias_planned",
            "qflash_hip_last_error",
            "qflash_hip_mfma_layout_check", "qflash_hip_lut_bounds", "qflash_hip_set_test_hooks",
            "qflash_hip_version")
@@ -43,6 +44,9 @@ HOOKS = {"FORCE_GENERAL": 1, "FORCE_DYNAMIC_BOUND": 2, "FORCE_ROBUST": 4, "NO_LU
 # element type codes of qflash_hip_scales / qflash_hip_quantize, and its workspace
 F32, F16, BF16, I8 = 0, 1, 2, 3
 SCALES_WORKSPACE = 256
+# device parameter block of qflash_hip_constants and its status codes
+PARAMS_WORDS = 16
+STATUS_ZERODIV_SCALE, STATUS_NAN, STATUS_INF, STATUS_ZERODIV_RSCALE, STATUS_RANGE = 1, 2, 3, 4, 5
 
 E_HEADDIM = -2
 
@@ -71,6 +75,14 @@ def _declare(L):
     L.qflash_hip_window_bias.argtypes = [vp, vp, i32, i32, i32, ctypes.c_double, vp, vp]
     L.qflash_hip_mask_bias.restype = ctypes.c_int
     L.qflash_hip_mask_bias.argtypes = [vp, ctypes.c_int64, ctypes.c_double, vp, vp]
+    L.qflash_hip_constants.restype = ctypes.c_int
+    L.qflash_hip_constants.argtypes = [vp, i32, ctypes.c_double, i32, i32, i32, fp, vp, vp]
+    L.qflash_hip_forward_planned.restype = ctypes.c_int
+    L.qflash_hip_forward_planned.argtypes = [vp, vp, vp, vp, i32, vp, vp, i32, vp, i64p, i32, i32, i32, i32, fp, vp]
+    L.qflash_hip_window_bias_planned.restype = ctypes.c_int
+    L.qflash_hip_window_bias_planned.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp]
+    L.qflash_hip_mask_bias_planned.restype = ctypes.c_int
+    L.qflash_hip_mask_bias_planned.argtypes = [vp, ctypes.c_int64, vp, vp, vp]
     L.qflash_hip_forward.restype = ctypes.c_int
     L.qflash_hip_forward.argtypes = [vp, vp, vp, vp, i32, vp, vp, i32, i32, i32, i32, i32, i32, i64p, i32, i32, i32,
                                      i32, fp, vp]

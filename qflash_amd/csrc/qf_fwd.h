@@ -89,7 +89,33 @@ struct Args {
     void* out_t;
     int32_t out_dt;
     const void* o_scale;
+    // constants and fast-path plan in device memory (qflash_hip_constants), or
+    // nullptr: then the fields above hold them
+    const int32_t* params;
+    int32_t general_only;  // with params: the general kernel runs whatever the plan says (layout)
 };
+
+// Words of the device parameter block written by qflash_hip_constants.
+enum ParamWord : int {
+    kPStatus = 0, kPRs, kPEm, kPRm, kPLm, kPAm, kPFast, kPIdOk, kPXSafe, kPEpsAbs, kPEAcc, kPLutN, kPLutLim,
+    kPSmScale = 14  // double, words 14-15
+};
+
+// The constants and plan fields of `a` from its device parameter block.
+__device__ __forceinline__ void load_params(Args& a) {
+    const int32_t* p = a.params;
+    a.rs = p[kPRs];
+    a.eM = p[kPEm];
+    a.rM = p[kPRm];
+    a.lM = p[kPLm];
+    a.aM = p[kPAm];
+    a.id_ok = p[kPIdOk];
+    a.x_safe = p[kPXSafe];
+    a.eps_abs = p[kPEpsAbs];
+    a.e_acc = p[kPEAcc];
+    a.lut_n = p[kPLutN];
+    a.lut_lim = p[kPLutLim];
+}
 
 __device__ __forceinline__ int out_esize(int dt) { return dt == QFLASH_HIP_I8 ? 1 : (dt == QFLASH_HIP_F32 ? 4 : 2); }
 
@@ -270,6 +296,10 @@ __device__ __forceinline__ void stage_kv(const Args& a, const int8_t* kb, const 
 // arithmetic on every element: exact for any constants and inputs.
 template <int D, int W, bool MASKED, bool VEC>
 __global__ __launch_bounds__(64 * W) void fwd_general(Args a) {
+    if (a.params) {  // constants in device memory: runs unless they failed or the fast kernel serves them
+        if (a.params[kPStatus] != 0 || (!a.general_only && a.params[kPFast])) return;
+        load_params(a);
+    }
     using T = Tile<D>;
     constexpr int NT = 64 * W;
     constexpr int DB = D / 32;  // 32-column blocks of the head dimension
@@ -1363,6 +1393,25 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
     fast_block<D, W, MASKED, DYN>(a, smem, wg / a.mblocks, wg % a.mblocks);
 }
 
+// The fast kernel on constants in device memory (qflash_hip_constants): it
+// does nothing unless the plan admits the fast path; the identity proof of
+// the rescale (id_ok) selects between the two variants inside.
+template <int D, int W, bool MASKED>
+__global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast_planned(Args a) {
+    using S = Stage<D, W>;
+    __shared__ __attribute__((aligned(16))) int8_t smem[2 * S::BYTES + kLutMax];
+    if (a.params[kPStatus] != 0 || !a.params[kPFast]) return;
+    load_params(a);
+    for (int u = threadIdx.x; u < a.lut_n; u += 64 * W)
+        smem[2 * S::BYTES + a.lut_n - 1 - u] =
+            (int8_t)(mad24(exp2_fast(-u, a.eM, a.rs), a.rM, 1 << 15) >> 16);
+    const int wg = xcd_order(blockIdx.x, a.n_wg);
+    if (a.id_ok)
+        fast_block<D, W, MASKED, false>(a, smem, wg / a.mblocks, wg % a.mblocks);
+    else
+        fast_block<D, W, MASKED, true>(a, smem, wg / a.mblocks, wg % a.mblocks);
+}
+
 
 
 // ----------------------------------------------------------------------------
@@ -1428,6 +1477,21 @@ static hipError_t launch_fast(const Args& a, int wg_per_cu, dim3 grid, hipStream
 
 template <int D, int W, bool MASKED>
 static hipError_t launch_dw(const Args& a, bool vec, bool fast, int wg_per_cu, dim3 grid, hipStream_t st) {
+    if (a.params) {
+        // constants in device memory: the fast kernel (when the layout admits it)
+        // and the general one, each returning at once unless the plan selects it
+        if constexpr (D <= 128) {
+            if (fast) {
+                hipLaunchKernelGGL((fwd_fast_planned<D, W, MASKED>), grid, dim3(64 * W), 0, st, a);
+                if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+            }
+        }
+        if (vec)
+            hipLaunchKernelGGL((fwd_general<D, W, MASKED, true>), grid, dim3(64 * W), 0, st, a);
+        else
+            hipLaunchKernelGGL((fwd_general<D, W, MASKED, false>), grid, dim3(64 * W), 0, st, a);
+        return hipGetLastError();
+    }
     if constexpr (D <= 128) {
         // DYN: the identity of the rescale by alpha = rs is proved per row in-kernel
         if (fast) return a.id_ok ? launch_fast<D, W, MASKED, false>(a, wg_per_cu, grid, st)

@@ -72,20 +72,29 @@ static bool hook(uint32_t bit) { return (g_hook_bits.load(std::memory_order_rela
 // n entries p(0 .. n - 1), the last one 0, and lim such that p(u) = 0 for
 // every u in [n - 1, lim].  From u0 on (q >= bitlen(rs) + 3) the bound of
 // lut_pack_vt's comment gives E = 0 up to lim; below u0 the values are
-// computed here, with the kernel's own integer primitives.  n = 0: no table.
-static void lut_bounds(const Args& a, int32_t* n_out, int32_t* lim_out) {
-    *n_out = 0;
-    *lim_out = 0;
+// computed with the kernel's own integer primitives (lut_scan).  n = 0: no
+// table.  lut_range returns u0 (or -1: no table) and sets lim.
+__host__ __device__ static int64_t lut_range(const Args& a, int64_t* lim_out) {
     const int64_t A = -(int64_t)a.eM, rs = a.rs;
-    if (!a.exp_mode || A <= 0 || rs <= 0) return;
+    if (!a.exp_mode || A <= 0 || rs <= 0) return -1;
     const int64_t kap = A * rs - 65536;
-    if (kap > 2 * A) return;
+    if (kap > 2 * A) return -1;
     int64_t lim = (int64_t)INT32_MAX / A;              // u * |eM| < 2^31: x * eM does not wrap
     if (kap < 0 && rs * 65536 / -kap < lim) lim = rs * 65536 / -kap;  // r >= -2 rs
     int bl = 0;
     while ((1ll << bl) <= rs) ++bl;
     const int64_t u0 = ((bl + 3) * 65536 + A - 1) / A;  // q >= bitlen(rs) + 3 for u >= u0
-    if (u0 > lim || u0 >= kLutMax) return;
+    if (u0 > lim || u0 >= kLutMax) return -1;
+    *lim_out = lim;
+    return u0;
+}
+
+static void lut_bounds(const Args& a, int32_t* n_out, int32_t* lim_out) {
+    *n_out = 0;
+    *lim_out = 0;
+    int64_t lim = 0;
+    const int64_t u0 = lut_range(a, &lim);
+    if (u0 < 0) return;
     int64_t n = 1;
     for (int64_t u = u0; u >= 0; --u)
         if (requant(exp2_i32((int32_t)-u, a), a) != 0) {
@@ -96,19 +105,22 @@ static void lut_bounds(const Args& a, int32_t* n_out, int32_t* lim_out) {
     *lim_out = (int32_t)lim;
 }
 
-// The table for this call, or none (lut_n = 0).  Filling it costs each
-// workgroup a few hundred VALU operations and every step an LDS round trip,
-// so it is used for rows of at least 4 steps in grids of at least two rounds
-// of waves (measured on MI355X: 8% slower at ViT-S 197 x 64 x 6 heads x 64,
-// one round; 9% faster at ViT-B/384, 3.75 rounds).
+// Whether the table pays for this launch (test hooks aside): filling it costs
+// each workgroup a few hundred VALU operations and every step an LDS round
+// trip; it replaces ~80 VALU instructions per 32-key step, and filling it
+// costs each wave ~10 per 64 * W entries (measured on MI355X: worth it for
+// every N >= 32).
+__host__ __device__ static bool lut_wanted(const Args& a, bool no_lut, bool force_lut) {
+    if (a.force_robust || no_lut) return false;
+    return a.N >= 32 || force_lut;
+}
+
+// The table for this call, or none (lut_n = 0).
 static void choose_lut(Args& a, int W) {
     a.lut_n = 0;
     a.lut_lim = 0;
-    if (a.force_robust || hook(QFLASH_HIP_HOOK_NO_LUT)) return;  // test hooks
-    // the table replaces ~80 VALU instructions per 32-key step, and filling it
-    // costs each wave ~10 per 64 * W entries
-    const bool pays = a.N >= 32;
-    if (!pays && !hook(QFLASH_HIP_HOOK_FORCE_LUT)) return;
+    (void)W;
+    if (!lut_wanted(a, hook(QFLASH_HIP_HOOK_NO_LUT), hook(QFLASH_HIP_HOOK_FORCE_LUT))) return;
     int32_t n, lim;
     lut_bounds(a, &n, &lim);
     if (n - 1 > a.x_safe) return;  // the kernel fills the table with the 24-bit E
@@ -116,17 +128,11 @@ static void choose_lut(Args& a, int W) {
     a.lut_lim = lim;
 }
 
-// Proof obligations of fwd_fast (see the comment above it).  Returns true and
-// fills a.x_safe / a.id_ok when the fast path computes exactly what the
-// reference does for every possible int8 input of this shape.
-static bool choose_fast(Args& a, int D, bool masked, bool vec) {
-    if (D > 128) return false;  // D=256 would spill: the general kernel serves it
-    if (!vec || a.so[3] != 1) return false;
-    // buffer accesses of K, V (loads) and O (stores): rows >= N must fall past
-    // (N-1)*stride + D, and the last stage's offsets (keys < N + 128, stages of
-    // at most 128 keys) fit 31 bits
-    for (int64_t st : {a.sk[2], a.sv[2], a.so[2]})
-        if (st < D || (int64_t)(a.N + 128) * st + D > INT32_MAX) return false;
+// Proof obligations of fwd_fast on the constants (see the comment above it).
+// Returns true and fills a.x_safe / a.id_ok / a.eps_abs / a.e_acc when the
+// fast path computes exactly what the reference does for every possible int8
+// input of this shape, given a layout the fast kernel accepts (fast_layout).
+__host__ __device__ static bool fast_consts(Args& a, bool masked) {
     if (!a.exp_mode || !a.acc_mode || !a.l_mode) return false;
     if (a.acc_shift < 1 || a.acc_shift > 30 || a.l_shift < 1 || a.l_shift > 30) return false;
     if ((int64_t)a.rs * a.aM >= (1ll << 31) || (int64_t)a.rs * a.lM >= (1ll << 31)) return false;
@@ -156,12 +162,111 @@ static bool choose_fast(Args& a, int D, bool masked, bool vec) {
     return true;
 }
 
+// Layouts the fast kernel accepts (unit column stride, 16-byte rows, buffer
+// offsets in 31 bits).
+static bool fast_layout(const Args& a, int D, bool vec) {
+    if (D > 128) return false;  // D=256 would spill: the general kernel serves it
+    if (!vec || a.so[3] != 1) return false;
+    // buffer accesses of K, V (loads) and O (stores): rows >= N must fall past
+    // (N-1)*stride + D, and the last stage's offsets (keys < N + 128, stages of
+    // at most 128 keys) fit 31 bits
+    for (int64_t st : {a.sk[2], a.sv[2], a.so[2]})
+        if (st < D || (int64_t)(a.N + 128) * st + D > INT32_MAX) return false;
+    return true;
+}
+
+static bool choose_fast(Args& a, int D, bool masked, bool vec) {
+    return fast_layout(a, D, vec) && fast_consts(a, masked);
+}
+
+// ---- constants on the device (qflash_hip_constants) --------------------------
+// qflash/kernel.py:297-307 in Python's double arithmetic: sm_scale = scale *
+// float(q_scale * k_scale), then each constant int(round(...)) (round half to
+// even = rint), evaluated in the reference's order so that the first failure
+// is the exception Python raises there; then every constant must fit int32.
+__device__ static double scale_value_f64(const void* p, int dt) {
+    if (dt == QFLASH_HIP_F32) return (double)*reinterpret_cast<const float*>(p);
+    const uint32_t h = *reinterpret_cast<const uint16_t*>(p);
+    return (double)(dt == QFLASH_HIP_F16 ? __half2float(__ushort_as_half((unsigned short)h)) : __uint_as_float(h << 16));
+}
+
+// round() of a finite double as Python's int: status 0, or the exception
+__device__ static int py_round(double x, double* r) {
+    if (__builtin_isnan(x)) return QFLASH_HIP_STATUS_NAN;
+    if (__builtin_isinf(x)) return QFLASH_HIP_STATUS_INF;
+    *r = __builtin_rint(x);
+    return 0;
+}
+
+__device__ static int device_constants(double sm, int l_shift, int acc_shift, int32_t* c) {
+    double v[5];
+    if (sm == 0.0) return QFLASH_HIP_STATUS_ZERODIV_SCALE;  // 1.0 / sm_scale
+    int st = py_round(1.0 / sm, &v[0]);                     // sm_rscale
+    if (!st) st = py_round(-sm * 65536.0, &v[1]);           // exp_M
+    if (!st) st = py_round(sm * 127.0 * 65536.0, &v[2]);    // req_M (left to right)
+    if (st) return st;
+    if (v[0] == 0.0) return QFLASH_HIP_STATUS_ZERODIV_RSCALE;  // (1 << shift) / sm_rscale
+    // int / int true division: correctly rounded, as IEEE division of the exact
+    // operands is while |sm_rscale| < 2^53 (larger ones fail the int32 test anyway)
+    v[3] = __builtin_rint(__builtin_ldexp(1.0, l_shift) / v[0]);
+    v[4] = __builtin_rint(__builtin_ldexp(1.0, acc_shift) / v[0]);
+    for (int i = 0; i < 5; ++i) {
+        if (!(v[i] >= -2147483648.0 && v[i] <= 2147483647.0)) return QFLASH_HIP_STATUS_RANGE;
+        c[i] = (int32_t)v[i];
+    }
+    return 0;
+}
+
+// One wave: lane 0 forms the constants and the plan; the table scan of
+// lut_bounds runs over the lanes.
+__global__ __launch_bounds__(64) void constants_kernel(const void* scales, int32_t dt, double scale, Args a,
+                                                       int32_t masked, uint32_t hooks, int32_t* params) {
+    const int lane = threadIdx.x;
+    const double sm = scale * scale_value_f64(static_cast<const char*>(scales) + 3 * (dt == QFLASH_HIP_F32 ? 4 : 2),
+                                              dt);
+    int32_t c[5] = {0, 0, 0, 0, 0};
+    const int status = device_constants(sm, a.l_shift, a.acc_shift, c);
+    a.rs = c[0]; a.eM = c[1]; a.rM = c[2]; a.lM = c[3]; a.aM = c[4];
+    a.id_ok = a.x_safe = a.eps_abs = a.e_acc = a.lut_n = a.lut_lim = 0;
+    bool fast = false;
+    if (status == 0) {
+        fast = !(hooks & QFLASH_HIP_HOOK_FORCE_GENERAL) && fast_consts(a, masked != 0);
+        if (fast && lut_wanted(a, hooks & QFLASH_HIP_HOOK_NO_LUT, hooks & QFLASH_HIP_HOOK_FORCE_LUT)) {
+            int64_t lim = 0;
+            const int64_t u0 = lut_range(a, &lim);
+            // largest u <= u0 (< kLutMax) with p(u) != 0, over the lanes
+            int32_t hit = -1;
+            for (int32_t u = (int32_t)u0 - lane; u >= 0; u -= 64)
+                if (requant(exp2_i32(-u, a), a) != 0) {
+                    hit = u;
+                    break;
+                }
+            for (int o = 32; o >= 1; o >>= 1) hit = max(hit, __shfl_xor(hit, o));
+            const int64_t n = hit >= 0 ? hit + 2 : 1;
+            if (u0 >= 0 && n - 1 <= a.x_safe) {
+                a.lut_n = (int32_t)n;
+                a.lut_lim = (int32_t)lim;
+            }
+        }
+        if (hooks & QFLASH_HIP_HOOK_FORCE_DYNAMIC_BOUND) a.id_ok = 0;
+    }
+    if (lane == 0) {
+        int32_t w[16] = {status, a.rs, a.eM, a.rM, a.lM, a.aM, fast ? 1 : 0, a.id_ok, a.x_safe, a.eps_abs, a.e_acc,
+                         a.lut_n, a.lut_lim, 0, 0, 0};
+        const uint64_t smb = __double_as_longlong(sm);
+        w[kPSmScale] = (int32_t)(uint32_t)smb;
+        w[kPSmScale + 1] = (int32_t)(uint32_t)(smb >> 32);
+        for (int i = 0; i < QFLASH_HIP_PARAMS_WORDS; ++i) params[i] = w[i];
+    }
+}
+
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 static int forward(const int8_t* Q, const int8_t* K, const int8_t* V, void* O, const int32_t* bias,
                    int32_t rs, int32_t eM, int32_t rM, int32_t lM, int32_t aM, const int64_t* strides,
                    int32_t Z, int32_t H, int32_t N, int32_t D, const qflash_hip_flags* flags, void* stream,
-                   int32_t bias_zmod = 0, int32_t out_dt = QFLASH_HIP_I8, const void* o_scale = nullptr) {
+                   int32_t bias_zmod = 0, int32_t out_dt = QFLASH_HIP_I8, const void* o_scale = nullptr,
+                   const int32_t* params = nullptr) {
     g_err[0] = 0;
     if (!Q || !K || !V || !O || !strides) return fail(QFLASH_HIP_EINVAL, "null pointer argument");
     if (out_dt != QFLASH_HIP_I8 && out_dt != QFLASH_HIP_F32 && out_dt != QFLASH_HIP_F16 && out_dt != QFLASH_HIP_BF16)
@@ -176,7 +281,7 @@ static int forward(const int8_t* Q, const int8_t* K, const int8_t* V, void* O, c
     // rs = round(1/sm_scale) is never 0 at the reference's launch (its host
     // divides by it, kernel.py:306); a negative one (negative `scale`) runs the
     // general kernel, exact for any constants
-    if (rs == 0) return fail(QFLASH_HIP_EINVAL, "sm_rscale must not be 0");
+    if (!params && rs == 0) return fail(QFLASH_HIP_EINVAL, "sm_rscale must not be 0");
     qflash_hip_flags f = {1, 1, 1, 30, 30};
     if (flags) f = *flags;
     if (f.l_use_shift && (f.l_shift < 1 || f.l_shift > 62))
@@ -235,9 +340,16 @@ static int forward(const int8_t* Q, const int8_t* K, const int8_t* V, void* O, c
     // not need them; NO_LUT / FORCE_LUT turn its table path off / on whatever
     // the shape.
     a.force_robust = hook(QFLASH_HIP_HOOK_FORCE_ROBUST) ? 1 : 0;
-    const bool fast = choose_fast(a, D, masked, vec) && !hook(QFLASH_HIP_HOOK_FORCE_GENERAL);
-    if (fast) choose_lut(a, W);
-    if (hook(QFLASH_HIP_HOOK_FORCE_DYNAMIC_BOUND)) a.id_ok = 0;
+    bool fast;
+    if (params) {  // the constants and their part of the plan are in device memory
+        a.params = params;
+        fast = fast_layout(a, D, vec) && !hook(QFLASH_HIP_HOOK_FORCE_GENERAL);
+        a.general_only = fast ? 0 : 1;
+    } else {
+        fast = choose_fast(a, D, masked, vec) && !hook(QFLASH_HIP_HOOK_FORCE_GENERAL);
+        if (fast) choose_lut(a, W);
+        if (hook(QFLASH_HIP_HOOK_FORCE_DYNAMIC_BOUND)) a.id_ok = 0;
+    }
     dim3 grid((unsigned)nwg);
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;
@@ -298,6 +410,47 @@ int qflash_hip_forward(const int8_t* Q, const int8_t* K, const int8_t* V, void* 
         return qf::fail(QFLASH_HIP_EINVAL, "bias_zmod %d needs a bias (>= 0)", bias_zmod);
     return qf::forward(Q, K, V, Out, attn_bias, sm_rscale, exp_M, req_M, l_M, acc_M, strides, Z, H, N_CTX, HEAD_DIM,
                        flags, stream, bias_zmod, out_dtype, o_scale);
+}
+
+int qflash_hip_constants(const void* scales, int32_t dtype, double scale, int32_t N_CTX, int32_t HEAD_DIM,
+                         int32_t masked, const qflash_hip_flags* flags, int32_t* params, void* stream) {
+    qf::g_err[0] = 0;
+    if (!scales || !params) return qf::fail(QFLASH_HIP_EINVAL, "null pointer argument");
+    if (dtype != QFLASH_HIP_F32 && dtype != QFLASH_HIP_F16 && dtype != QFLASH_HIP_BF16)
+        return qf::fail(QFLASH_HIP_EINVAL, "unknown dtype code %d", dtype);
+    if (N_CTX <= 0 || HEAD_DIM <= 0) return qf::fail(QFLASH_HIP_EINVAL, "bad N_CTX=%d HEAD_DIM=%d", N_CTX, HEAD_DIM);
+    if (((uintptr_t)params & 7u) != 0) return qf::fail(QFLASH_HIP_EINVAL, "params must be 8-byte aligned");
+    qflash_hip_flags f = {1, 1, 1, 30, 30};
+    if (flags) f = *flags;
+    if (f.l_use_shift && (f.l_shift < 1 || f.l_shift > 62))
+        return qf::fail(QFLASH_HIP_EINVAL, "l_shift %d outside 1..62", f.l_shift);
+    if (f.acc_use_shift && (f.acc_shift < 1 || f.acc_shift > 62))
+        return qf::fail(QFLASH_HIP_EINVAL, "acc_shift %d outside 1..62", f.acc_shift);
+    qf::Args a{};
+    a.N = N_CTX;
+    a.l_shift = f.l_shift;
+    a.acc_shift = f.acc_shift;
+    a.exp_mode = f.exp_use_shift != 0;
+    a.l_mode = f.l_use_shift != 0;
+    a.acc_mode = f.acc_use_shift != 0;
+    const uint32_t hooks = qf::g_hook_bits.load(std::memory_order_relaxed);
+    a.force_robust = (hooks & QFLASH_HIP_HOOK_FORCE_ROBUST) ? 1 : 0;
+    hipLaunchKernelGGL(qf::constants_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, scales, dtype, scale, a,
+                       masked ? 1 : 0, hooks, params);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return qf::fail(QFLASH_HIP_ELAUNCH, "launch failed: %s", hipGetErrorString(e));
+    return QFLASH_HIP_OK;
+}
+
+int qflash_hip_forward_planned(const int8_t* Q, const int8_t* K, const int8_t* V, void* Out, int32_t out_dtype,
+                               const void* o_scale, const int32_t* attn_bias, int32_t bias_zmod,
+                               const int32_t* params, const int64_t* strides, int32_t Z, int32_t H, int32_t N_CTX,
+                               int32_t HEAD_DIM, const qflash_hip_flags* flags, void* stream) {
+    if (!params) return qf::fail(QFLASH_HIP_EINVAL, "params is null");
+    if (bias_zmod < 0 || (bias_zmod > 0 && !attn_bias))
+        return qf::fail(QFLASH_HIP_EINVAL, "bias_zmod %d needs a bias (>= 0)", bias_zmod);
+    return qf::forward(Q, K, V, Out, attn_bias, 0, 0, 0, 0, 0, strides, Z, H, N_CTX, HEAD_DIM, flags, stream,
+                       bias_zmod, out_dtype, o_scale, params);
 }
 
 const char* qflash_hip_last_error(void) { return qf::g_err; }

@@ -480,11 +480,22 @@ __device__ __forceinline__ int32_t bias_of(float x, float log2e, float inv_sm) {
     return masked ? kNegInfBias : (int32_t)rintf(y);
 }
 
+// RN_fp32(1 / RN_fp32(sm_scale)) from the double at words 14-15 of a device
+// parameter block (qflash_hip_constants), as the host forms it.
+__device__ __forceinline__ float inv_sm_of(const int32_t* params) {
+    const uint64_t b = (uint32_t)params[14] | ((uint64_t)(uint32_t)params[15] << 32);
+    return __fdiv_rn(1.0f, (float)__longlong_as_double((long long)b));
+}
+
 __global__ __launch_bounds__(256) void window_bias_kernel(const float* rel, const float* mask, int32_t H,
                                                            int32_t nn, int64_t total, float log2e, float inv_sm,
-                                                           int32_t* out) {
+                                                           const int32_t* params, int32_t* out) {
     const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (e >= total) return;
+    if (params) {
+        if (params[0] != 0) return;
+        inv_sm = inv_sm_of(params);
+    }
     const int32_t ij = (int32_t)(e % nn), wh = (int32_t)(e / nn);
     const int32_t h = wh % H, w = wh / H;
     float x = rel[(int64_t)h * nn + ij];
@@ -495,8 +506,12 @@ __global__ __launch_bounds__(256) void window_bias_kernel(const float* rel, cons
 // qflash_hip_mask_bias: four elements per thread, 16-byte loads and stores
 // when both buffers are 16-byte aligned.
 __global__ __launch_bounds__(256) void mask_bias_kernel(const float* mask, int64_t n, bool vec, float log2e,
-                                                         float inv_sm, int32_t* out) {
+                                                         float inv_sm, const int32_t* params, int32_t* out) {
     const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (params) {
+        if (params[0] != 0) return;
+        inv_sm = inv_sm_of(params);
+    }
     if (vec && i + 4 <= n) {
         const float4 x = *reinterpret_cast<const float4*>(mask + i);
         *reinterpret_cast<int4*>(out + i) = int4{bias_of(x.x, log2e, inv_sm), bias_of(x.y, log2e, inv_sm),
@@ -611,40 +626,65 @@ int qflash_hip_quantize(const void* q, const void* k, const void* v, int32_t dty
     }
 }
 
-int qflash_hip_window_bias(const float* rel, const float* mask, int32_t n_win, int32_t H, int32_t N,
-                           double sm_scale, int32_t* out, void* stream) {
-    qfq::g_err[0] = 0;
-    if (!rel || !out) return qfq::fail(QFLASH_HIP_EINVAL, "null pointer argument");
+namespace qfq {
+static int window_bias(const float* rel, const float* mask, int32_t n_win, int32_t H, int32_t N, double sm_scale,
+                       const int32_t* params, int32_t* out, void* stream) {
+    g_err[0] = 0;
+    if (!rel || !out) return fail(QFLASH_HIP_EINVAL, "null pointer argument");
     if (H <= 0 || N <= 0 || n_win <= 0 || (!mask && n_win != 1))
-        return qfq::fail(QFLASH_HIP_EINVAL, "bad window bias shape nW=%d H=%d N=%d%s", n_win, H, N,
-                         mask ? "" : " (no mask: nW must be 1)");
-    if (!(sm_scale != 0.0) || !(fabs(sm_scale) < 1e30)) return qfq::fail(QFLASH_HIP_EINVAL, "bad sm_scale %g", sm_scale);
+        return fail(QFLASH_HIP_EINVAL, "bad window bias shape nW=%d H=%d N=%d%s", n_win, H, N,
+                    mask ? "" : " (no mask: nW must be 1)");
+    if (!params && (!(sm_scale != 0.0) || !(fabs(sm_scale) < 1e30)))
+        return fail(QFLASH_HIP_EINVAL, "bad sm_scale %g", sm_scale);
     const int64_t nn = (int64_t)N * N, total = (int64_t)n_win * H * nn;
-    if (total >= ((int64_t)1 << 31)) return qfq::fail(QFLASH_HIP_EINVAL, "window bias too large");
+    if (total >= ((int64_t)1 << 31)) return fail(QFLASH_HIP_EINVAL, "window bias too large");
     // torch: x * LOG2E and x / sm_scale with host scalars, both taken to fp32
     // (the division as a product with the fp32 reciprocal of the fp32 divisor)
     const float log2e = (float)1.44269504;
-    const float inv_sm = 1.0f / (float)sm_scale;
-    hipLaunchKernelGGL(qfq::window_bias_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                       (hipStream_t)stream, rel, mask, H, (int32_t)nn, total, log2e, inv_sm, out);
+    const float inv_sm = params ? 0.0f : 1.0f / (float)sm_scale;
+    hipLaunchKernelGGL(window_bias_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       rel, mask, H, (int32_t)nn, total, log2e, inv_sm, params, out);
     if (hipError_t err = hipGetLastError(); err != hipSuccess)
-        return qfq::fail(QFLASH_HIP_ELAUNCH, "window bias launch: %s", hipGetErrorString(err));
+        return fail(QFLASH_HIP_ELAUNCH, "window bias launch: %s", hipGetErrorString(err));
     return 0;
 }
 
-int qflash_hip_mask_bias(const float* mask, int64_t n, double sm_scale, int32_t* out, void* stream) {
-    qfq::g_err[0] = 0;
-    if (!mask || !out) return qfq::fail(QFLASH_HIP_EINVAL, "null pointer argument");
-    if (n <= 0 || n >= ((int64_t)1 << 31)) return qfq::fail(QFLASH_HIP_EINVAL, "bad mask size %lld", (long long)n);
-    if (!(sm_scale != 0.0) || !(fabs(sm_scale) < 1e30)) return qfq::fail(QFLASH_HIP_EINVAL, "bad sm_scale %g", sm_scale);
+static int mask_bias(const float* mask, int64_t n, double sm_scale, const int32_t* params, int32_t* out,
+                     void* stream) {
+    g_err[0] = 0;
+    if (!mask || !out) return fail(QFLASH_HIP_EINVAL, "null pointer argument");
+    if (n <= 0 || n >= ((int64_t)1 << 31)) return fail(QFLASH_HIP_EINVAL, "bad mask size %lld", (long long)n);
+    if (!params && (!(sm_scale != 0.0) || !(fabs(sm_scale) < 1e30)))
+        return fail(QFLASH_HIP_EINVAL, "bad sm_scale %g", sm_scale);
     const float log2e = (float)1.44269504;
-    const float inv_sm = 1.0f / (float)sm_scale;
+    const float inv_sm = params ? 0.0f : 1.0f / (float)sm_scale;
     const bool vec = (((uintptr_t)mask | (uintptr_t)out) & 15u) == 0;
-    hipLaunchKernelGGL(qfq::mask_bias_kernel, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0,
-                       (hipStream_t)stream, mask, n, vec, log2e, inv_sm, out);
+    hipLaunchKernelGGL(mask_bias_kernel, dim3((unsigned)((n + 1023) / 1024)), dim3(256), 0, (hipStream_t)stream, mask,
+                       n, vec, log2e, inv_sm, params, out);
     if (hipError_t err = hipGetLastError(); err != hipSuccess)
-        return qfq::fail(QFLASH_HIP_ELAUNCH, "mask bias launch: %s", hipGetErrorString(err));
+        return fail(QFLASH_HIP_ELAUNCH, "mask bias launch: %s", hipGetErrorString(err));
     return 0;
+}
+}  // namespace qfq
+
+int qflash_hip_window_bias(const float* rel, const float* mask, int32_t n_win, int32_t H, int32_t N,
+                           double sm_scale, int32_t* out, void* stream) {
+    return qfq::window_bias(rel, mask, n_win, H, N, sm_scale, nullptr, out, stream);
+}
+
+int qflash_hip_window_bias_planned(const float* rel, const float* mask, int32_t n_win, int32_t H, int32_t N,
+                                   const int32_t* params, int32_t* out, void* stream) {
+    if (!params) return qfq::fail(QFLASH_HIP_EINVAL, "params is null");
+    return qfq::window_bias(rel, mask, n_win, H, N, 0.0, params, out, stream);
+}
+
+int qflash_hip_mask_bias(const float* mask, int64_t n, double sm_scale, int32_t* out, void* stream) {
+    return qfq::mask_bias(mask, n, sm_scale, nullptr, out, stream);
+}
+
+int qflash_hip_mask_bias_planned(const float* mask, int64_t n, const int32_t* params, int32_t* out, void* stream) {
+    if (!params) return qfq::fail(QFLASH_HIP_EINVAL, "params is null");
+    return qfq::mask_bias(mask, n, 0.0, params, out, stream);
 }
 
 }  // extern "C"

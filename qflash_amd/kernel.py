@@ -384,6 +384,125 @@ def launch_forward(q8: Tensor, k8: Tensor, v8: Tensor, out: Tensor, consts, flag
     _lib.check(rc, "qflash_hip_forward")
 
 
+def _flags():
+    return _lib.Flags(int(EXP_USE_SHIFT), int(L_USE_SHIFT), int(ACC_USE_SHIFT), int(L_SHIFT), int(ACC_SHIFT))
+
+
+def _flag_kw():
+    return dict(EXP_USE_SHIFT=EXP_USE_SHIFT, L_USE_SHIFT=L_USE_SHIFT, ACC_USE_SHIFT=ACC_USE_SHIFT,
+                L_SHIFT=L_SHIFT, ACC_SHIFT=ACC_SHIFT)
+
+
+def device_constants(scales: Tensor, scale: float, N: int, D: int, masked: bool) -> Tensor:
+    """The fixed-point constants on the device (qflash_hip_constants): a device
+    int32 block of _lib.PARAMS_WORDS words holding a status (0, or the
+    exception the reference's host would raise, see raise_status), sm_rscale,
+    exp_M, req_M, l_M, acc_M (kernel.py:297-307, Python's double arithmetic),
+    the fast kernel's plan and sm_scale.  `scales` from quantize_qkv; `scale`
+    the host's (scale or 1/sqrt(D)) * LOG2E.  Asynchronous, no host sync."""
+    params = torch.empty(_lib.PARAMS_WORDS, dtype=torch.int32, device=scales.device)
+    fl = _flags()
+    _lib.check(_lib.load().qflash_hip_constants(ctypes.c_void_p(scales.data_ptr()), _DT_CODE[scales.dtype],
+                                                float(scale), int(N), int(D), int(masked), ctypes.byref(fl),
+                                                ctypes.c_void_p(params.data_ptr()), _stream_ptr(scales)),
+               "qflash_hip_constants")
+    return params
+
+
+def raise_status(status: int) -> None:
+    """Raise what the reference's host raises for the value that produced this
+    status of qflash_hip_constants (kernel.py:302-307, then the int32 check of
+    the launch); nothing for 0."""
+    if status == 0:
+        return
+    if status == _lib.STATUS_ZERODIV_SCALE:
+        raise ZeroDivisionError("float division by zero")
+    if status == _lib.STATUS_NAN:
+        raise ValueError("cannot convert float NaN to integer")
+    if status == _lib.STATUS_INF:
+        raise OverflowError("cannot convert float infinity to integer")
+    if status == _lib.STATUS_ZERODIV_RSCALE:
+        raise ZeroDivisionError("division by zero")
+    if status == _lib.STATUS_RANGE:
+        raise _lib.QFlashLibraryError("a fixed-point constant does not fit int32; the gfx950 kernels take int32 "
+                                      "constants")
+    raise _lib.QFlashLibraryError(f"qflash_hip_constants: unknown status {status}")
+
+
+def _status_check(params: Tensor):
+    """Eager mode: start copying the status word to pinned host memory and return
+    a function that waits for that copy only and raises the reference's
+    exception.  Under HIP graph capture: no copy, no check (nothing may
+    synchronise; a failing status leaves the outputs unwritten)."""
+    if torch.cuda.is_current_stream_capturing():
+        return lambda: None
+    wait = _scalar_to_host(params[0])
+    return lambda: raise_status(int(wait()))
+
+
+def mask_to_bias_planned(attn_mask: Tensor, params: Tensor, Z: int, H: int, N: int) -> Tensor:
+    """mask_to_bias with sm_scale read on the device from `params` (fp32 masks:
+    qflash_hip_mask_bias_planned; bool masks need no sm_scale)."""
+    if attn_mask.dtype == torch.bool:
+        return bias_values(attn_mask, 1.0).expand(Z, H, N, N)
+    m = attn_mask.contiguous()
+    b = torch.empty(m.shape, dtype=torch.int32, device=m.device)
+    _lib.check(_lib.load().qflash_hip_mask_bias_planned(ctypes.c_void_p(m.data_ptr()), m.numel(),
+                                                        ctypes.c_void_p(params.data_ptr()),
+                                                        ctypes.c_void_p(b.data_ptr()), _stream_ptr(m)),
+               "qflash_hip_mask_bias_planned")
+    return b.expand(Z, H, N, N)
+
+
+def window_bias_planned(rel_bias: Tensor, mask: Tensor | None, params: Tensor) -> Tensor:
+    """window_bias with sm_scale read on the device from `params` (fp32 tables)."""
+    H, N = rel_bias.shape[-3], rel_bias.shape[-1]
+    rel = rel_bias.reshape(H, N, N).contiguous()
+    m = None if mask is None else mask.contiguous()
+    n_win = 1 if m is None else m.shape[0]
+    out = torch.empty((n_win, H, N, N), dtype=torch.int32, device=rel.device)
+    _lib.check(_lib.load().qflash_hip_window_bias_planned(
+        ctypes.c_void_p(rel.data_ptr()), ctypes.c_void_p(0 if m is None else m.data_ptr()), n_win, H, N,
+        ctypes.c_void_p(params.data_ptr()), ctypes.c_void_p(out.data_ptr()), _stream_ptr(rel)),
+        "qflash_hip_window_bias_planned")
+    return out
+
+
+def launch_forward_planned(q8: Tensor, k8: Tensor, v8: Tensor, out: Tensor, params: Tensor,
+                           bias: Tensor | None = None, bias_zmod: int = 0, o_scale: Tensor | None = None) -> None:
+    """launch_forward with the constants in the device block `params`
+    (qflash_hip_forward_planned)."""
+    Z, H, N, D = q8.shape
+    if out.dtype == torch.int8:
+        code, sp = _lib.I8, None
+    else:
+        code = _DT_CODE[out.dtype]
+        sp = ctypes.c_void_p(o_scale.data_ptr())
+    fl = _flags()
+    bst = (0, 0, 0, 0) if bias is None else bias.stride()
+    st = (ctypes.c_int64 * 20)(*q8.stride(), *k8.stride(), *v8.stride(), *out.stride(), *bst)
+    bp = None if bias is None else ctypes.c_void_p(bias.data_ptr())
+    rc = _lib.load().qflash_hip_forward_planned(
+        ctypes.c_void_p(q8.data_ptr()), ctypes.c_void_p(k8.data_ptr()), ctypes.c_void_p(v8.data_ptr()),
+        ctypes.c_void_p(out.data_ptr()), code, sp, bp, int(bias_zmod), ctypes.c_void_p(params.data_ptr()), st, Z, H,
+        N, D, ctypes.byref(fl), _stream_ptr(q8))
+    _lib.check(rc, "qflash_hip_forward_planned")
+
+
+def _device_path(query: Tensor, key: Tensor, value: Tensor, attn_mask: Tensor | None) -> bool:
+    """Inputs whose whole forward runs on the device (constants included):
+    fp32 / fp16 / bf16 (Z, H, N, D) tensors of one dtype, and no mask, a bool
+    mask or an fp32 mask on the device."""
+    T = query.dtype
+    if T not in _DT_CODE or key.dtype != T or value.dtype != T:
+        return False
+    if query.dim() != 4 or key.dim() != 4 or value.dim() != 4:
+        return False
+    if attn_mask is None or attn_mask.dtype == torch.bool:
+        return True
+    return attn_mask.dtype == torch.float32 and attn_mask.is_cuda and 0 < attn_mask.numel() < (1 << 31)
+
+
 def qflash_forward(
     query: Tensor,
     key: Tensor,
@@ -398,6 +517,12 @@ def qflash_forward(
     attn_mask: None, bool (True = keep) or float additive mask broadcastable
     to (Z, H, N, N).  Returns ``o_int8 * o_scale`` in the input dtype, or the
     median kernel time in ms for return_mode='latency'.
+
+    fp32 / fp16 / bf16 inputs run entirely on the device, constants included
+    (no host synchronisation, so the call can be captured in a HIP graph);
+    in eager mode the exceptions the reference raises while forming its
+    constants are raised before the call returns.  Other dtypes follow the
+    reference's host sequence.
     """
     d_q, d_k, d_v = query.shape[-1], key.shape[-1], value.shape[-1]
     assert d_q == d_k and d_k == d_v
@@ -406,6 +531,11 @@ def qflash_forward(
     if scale is None:
         scale = 1.0 / (d_q ** 0.5)
     scale = scale * LOG2E
+    for x in (query, key, value):
+        if not x.is_cuda:
+            raise ValueError(f"qflash: all tensors must be on a GPU device (got {x.device})")
+    if _device_path(query, key, value, attn_mask):
+        return _forward_device(query, key, value, attn_mask, scale, return_mode)
 
     scales, finish = quantize_qkv(query, key, value)  # kernel.py:294-296 on the device
     o_scale = scales[2]
@@ -434,6 +564,26 @@ def qflash_forward(
     return o * o_scale
 
 
+def _forward_device(query: Tensor, key: Tensor, value: Tensor, attn_mask: Tensor | None, scale: float,
+                    return_mode: str):
+    """qflash_forward on the device: scales, constants, quantisation, bias,
+    attention with the dequantisation fused, in stream order."""
+    Z, H, N = query.shape[0], query.shape[1], query.shape[2]
+    scales, finish = quantize_qkv(query, key, value)           # kernel.py:294-296
+    params = device_constants(scales, scale, N, query.shape[-1], attn_mask is not None)  # kernel.py:297-307
+    check = _status_check(params)
+    q8, k8, v8 = finish()                                       # kernel.py:309-311
+    bias = None if attn_mask is None else mask_to_bias_planned(attn_mask, params, Z, H, N)  # kernel.py:327-336
+    if return_mode == 'latency':  # the kernel alone, int8 codes out (kernel.py:348-349)
+        check()
+        o = torch.empty_like(v8)
+        return bench_latency_ms(lambda: launch_forward_planned(q8, k8, v8, o, params, bias), device=query.device)
+    out = torch.empty_like(v8, dtype=scales.dtype)              # o * o_scale fused (kernel.py:351)
+    launch_forward_planned(q8, k8, v8, out, params, bias, o_scale=scales[2])
+    check()
+    return out
+
+
 def qflash_forward_window(query: Tensor, key: Tensor, value: Tensor, rel_bias: Tensor, mask: Tensor | None = None,
                           scale: float | None = None) -> Tensor:
     """QWindowAttention's attention call without the materialised mask.
@@ -451,6 +601,22 @@ def qflash_forward_window(query: Tensor, key: Tensor, value: Tensor, rel_bias: T
     if scale is None:
         scale = 1.0 / (d_q ** 0.5)
     scale = scale * LOG2E
+    Z, H, N = query.shape[0], query.shape[1], query.shape[2]
+    tables_fp32 = rel_bias.dtype == torch.float32 and rel_bias.is_cuda and (
+        mask is None or (mask.dtype == torch.float32 and mask.is_cuda))
+    if tables_fp32 and _device_path(query, key, value, None):
+        if mask is not None and Z % mask.shape[0]:
+            raise ValueError(f"batch {Z} is not a multiple of the {mask.shape[0]} windows of the mask")
+        scales, finish = quantize_qkv(query, key, value)
+        params = device_constants(scales, scale, N, d_q, True)
+        check = _status_check(params)
+        q8, k8, v8 = finish()
+        wb = window_bias_planned(rel_bias, mask, params)
+        bias, zmod = (wb.expand(Z, H, N, N), 0) if mask is None else (wb, mask.shape[0])
+        out = torch.empty_like(v8, dtype=scales.dtype)
+        launch_forward_planned(q8, k8, v8, out, params, bias, zmod, o_scale=scales[2])
+        check()
+        return out
     scales, finish = quantize_qkv(query, key, value)
     o_scale = scales[2]
     qk_scale = _scalar_to_host(scales[3])

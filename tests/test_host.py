@@ -204,3 +204,20 @@ def test_swin_golden_mask_decomposes_into_window_parts():
     shift[1] = _shift_mask()
     composed = rel + shift.view(1, 2, 1, 49, 49).expand(2, -1, 3, -1, -1).reshape(-1, 3, 49, 49)
     assert torch.equal(composed, full)
+
+
+def test_status_words_raise_the_reference_exceptions():
+    """The status of qflash_hip_constants maps to the exception the reference's
+    host raises for the same value (kernel.py:302-307), in its order."""
+    from qflash_amd.kernel import raise_status
+    raise_status(0)
+    for code, exc, value in ((_lib.STATUS_ZERODIV_SCALE, ZeroDivisionError, 0.0),
+                             (_lib.STATUS_NAN, ValueError, float("nan")),
+                             (_lib.STATUS_INF, OverflowError, float("inf")),
+                             (_lib.STATUS_ZERODIV_RSCALE, ZeroDivisionError, 2.0)):
+        with pytest.raises(exc):
+            raise_status(code)
+        with pytest.raises(exc):  # the host arithmetic on a value that produces it
+            fixed_point_constants(value, 30, 30)
+    with pytest.raises(_lib.QFlashLibraryError):
+        raise_status(_lib.STATUS_RANGE)
