@@ -294,24 +294,28 @@ __device__ __forceinline__ void stage_kv(const Args& a, const int8_t* kb, const 
 
 // The reference algorithm with general (wrapping, clamping, 64-bit) integer
 // arithmetic on every element: exact for any constants and inputs.
+// Workgroup id -> (head, query block) so that consecutive blocks of one head
+// run on the same XCD (workgroups are dealt to the 8 XCDs round-robin).
+__device__ __forceinline__ int xcd_order(int b, int n) {
+    const int per = n >> 3, rem = n & 7, x = b & 7, i = b >> 3;
+    return x < rem ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
+}
+
+// One workgroup of the general kernel: row block blk % mblocks of head
+// blk / mblocks, with LDS at smem (Tile<D>::BYTES).
 template <int D, int W, bool MASKED, bool VEC>
-__global__ __launch_bounds__(64 * W) void fwd_general(Args a) {
-    if (a.params) {  // constants in device memory: runs unless they failed or the fast kernel serves them
-        if (a.params[kPStatus] != 0 || (!a.general_only && a.params[kPFast])) return;
-        load_params(a);
-    }
+__device__ __forceinline__ void general_block(const Args& a, int blk, int8_t* smem) {
     using T = Tile<D>;
     constexpr int NT = 64 * W;
     constexpr int DB = D / 32;  // 32-column blocks of the head dimension
-    __shared__ __attribute__((aligned(16))) int8_t smem[T::BYTES];
     int8_t* lk = smem;
     int8_t* lvt = smem + T::KBYTES;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int lq = lane & 31, g = lane >> 5;
-    const int zh = blockIdx.x / a.mblocks;
-    const int mb = blockIdx.x % a.mblocks;
+    const int zh = blk / a.mblocks;
+    const int mb = blk % a.mblocks;
     const int z = zh / a.H, h = zh % a.H;
     const int q0 = (mb * W + wave) * 32;
     const bool active = q0 < a.N;
@@ -408,6 +412,20 @@ __global__ __launch_bounds__(64 * W) void fwd_general(Args a) {
             }
         }
     });
+}
+
+// Under a plan (constants in device memory: qflash_hip_constants) it runs
+// unless they failed or the fast kernel serves them.
+template <int D, int W, bool MASKED, bool VEC>
+__global__ __launch_bounds__(64 * W) void fwd_general(Args a) {
+    __shared__ __attribute__((aligned(16))) int8_t smem[Tile<D>::BYTES];
+    if (a.params) {
+        if (a.params[kPStatus] != 0 || (!a.general_only && a.params[kPFast])) return;
+        load_params(a);
+    }
+    // consecutive row blocks of a head on one XCD, as in the fast kernel: K and V
+    // of the head come from HBM once and then from that XCD's L2
+    general_block<D, W, MASKED, VEC>(a, xcd_order(blockIdx.x, a.n_wg), smem);
 }
 
 // ----------------------------------------------------------------------------
@@ -589,12 +607,6 @@ __device__ __forceinline__ void stage_sync() {
     __syncthreads();
 }
 
-// Workgroup id -> (head, query block) so that consecutive blocks of one head
-// run on the same XCD (workgroups are dealt to the 8 XCDs round-robin).
-__device__ __forceinline__ int xcd_order(int b, int n) {
-    const int per = n >> 3, rem = n & 7, x = b & 7, i = b >> 3;
-    return x < rem ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
-}
 
 __device__ __forceinline__ int32_t rescale_fast(int32_t x, int32_t A, int64_t half, int32_t sh) {
     const int64_t p = (int64_t)x * (int64_t)A + half;
@@ -1393,15 +1405,21 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
     fast_block<D, W, MASKED, DYN>(a, smem, wg / a.mblocks, wg % a.mblocks);
 }
 
-// The fast kernel on constants in device memory (qflash_hip_constants): it
-// does nothing unless the plan admits the fast path; the identity proof of
-// the rescale (id_ok) selects between the two variants inside.
+// The kernels on constants in device memory (qflash_hip_constants), for
+// layouts the fast kernel accepts: the plan selects the fast path (and, by
+// the identity proof of the rescale, id_ok, one of its two variants) or the
+// general one, in one launch.
 template <int D, int W, bool MASKED>
 __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast_planned(Args a) {
     using S = Stage<D, W>;
+    static_assert(Tile<D>::BYTES <= 2 * S::BYTES + kLutMax, "the general path's tiles fit the fast path's LDS");
     __shared__ __attribute__((aligned(16))) int8_t smem[2 * S::BYTES + kLutMax];
-    if (a.params[kPStatus] != 0 || !a.params[kPFast]) return;
+    if (a.params[kPStatus] != 0) return;
     load_params(a);
+    if (!a.params[kPFast]) {
+        general_block<D, W, MASKED, true>(a, xcd_order(blockIdx.x, a.n_wg), smem);
+        return;
+    }
     for (int u = threadIdx.x; u < a.lut_n; u += 64 * W)
         smem[2 * S::BYTES + a.lut_n - 1 - u] =
             (int8_t)(mad24(exp2_fast(-u, a.eM, a.rs), a.rM, 1 << 15) >> 16);
@@ -1478,12 +1496,12 @@ static hipError_t launch_fast(const Args& a, int wg_per_cu, dim3 grid, hipStream
 template <int D, int W, bool MASKED>
 static hipError_t launch_dw(const Args& a, bool vec, bool fast, int wg_per_cu, dim3 grid, hipStream_t st) {
     if (a.params) {
-        // constants in device memory: the fast kernel (when the layout admits it)
-        // and the general one, each returning at once unless the plan selects it
+        // constants in device memory: one kernel whose path the plan selects when
+        // the layout admits the fast kernel, the general kernel otherwise
         if constexpr (D <= 128) {
             if (fast) {
                 hipLaunchKernelGGL((fwd_fast_planned<D, W, MASKED>), grid, dim3(64 * W), 0, st, a);
-                if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+                return hipGetLastError();
             }
         }
         if (vec)

@@ -430,14 +430,36 @@ def raise_status(status: int) -> None:
 
 
 def _status_check(params: Tensor):
-    """Eager mode: start copying the status word to pinned host memory and return
-    a function that waits for that copy only and raises the reference's
-    exception.  Under HIP graph capture: no copy, no check (nothing may
-    synchronise; a failing status leaves the outputs unwritten)."""
+    """Call right after the constants kernel is queued.  Eager mode: returns a
+    function that copies the status word to pinned host memory on a side
+    stream (after the constants kernel: the launch stream goes straight on),
+    waits for that copy only and raises the reference's exception; call it
+    once the rest of the forward is queued.  Under HIP graph capture: no copy,
+    no check (nothing may synchronise; a failing status leaves the outputs
+    unwritten)."""
     if torch.cuda.is_current_stream_capturing():
         return lambda: None
-    wait = _scalar_to_host(params[0])
-    return lambda: raise_status(int(wait()))
+    done = torch.cuda.Event()
+    done.record(torch.cuda.current_stream(params.device))
+
+    def check():
+        side = _side_stream(params.device)
+        side.wait_event(done)
+        with torch.cuda.stream(side):
+            wait = _scalar_to_host(params[0])
+        raise_status(int(wait()))
+    return check
+
+
+def _side_stream(device) -> torch.cuda.Stream:
+    """This thread's side stream on `device` (default priority)."""
+    cache = getattr(_host_cache, "side", None)
+    if cache is None:
+        cache = _host_cache.side = {}
+    st = cache.get(device.index)
+    if st is None:
+        st = cache[device.index] = torch.cuda.Stream(device=device)
+    return st
 
 
 def mask_to_bias_planned(attn_mask: Tensor, params: Tensor, Z: int, H: int, N: int) -> Tensor:
@@ -570,9 +592,11 @@ def _forward_device(query: Tensor, key: Tensor, value: Tensor, attn_mask: Tensor
     attention with the dequantisation fused, in stream order."""
     Z, H, N = query.shape[0], query.shape[1], query.shape[2]
     scales, finish = quantize_qkv(query, key, value)           # kernel.py:294-296
+    # the quantisation needs only the scales: queued first, so that the device
+    # never waits for the host's later launches
+    q8, k8, v8 = finish()                                       # kernel.py:309-311
     params = device_constants(scales, scale, N, query.shape[-1], attn_mask is not None)  # kernel.py:297-307
     check = _status_check(params)
-    q8, k8, v8 = finish()                                       # kernel.py:309-311
     bias = None if attn_mask is None else mask_to_bias_planned(attn_mask, params, Z, H, N)  # kernel.py:327-336
     if return_mode == 'latency':  # the kernel alone, int8 codes out (kernel.py:348-349)
         check()
@@ -608,9 +632,9 @@ def qflash_forward_window(query: Tensor, key: Tensor, value: Tensor, rel_bias: T
         if mask is not None and Z % mask.shape[0]:
             raise ValueError(f"batch {Z} is not a multiple of the {mask.shape[0]} windows of the mask")
         scales, finish = quantize_qkv(query, key, value)
+        q8, k8, v8 = finish()
         params = device_constants(scales, scale, N, d_q, True)
         check = _status_check(params)
-        q8, k8, v8 = finish()
         wb = window_bias_planned(rel_bias, mask, params)
         bias, zmod = (wb.expand(Z, H, N, N), 0) if mask is None else (wb, mask.shape[0])
         out = torch.empty_like(v8, dtype=scales.dtype)
