@@ -14,7 +14,8 @@ resident in HBM.  Prints ONE JSON line:
 
   per_config cfg1..cfg5 (cfg4 also with the reference's materialised bias)
              x seeds 0, 1, 2: us/call, flushed us/call, TOPS, fractions of
-             the MFMA peak and of the roofline, SQNR, end-to-end us
+             the MFMA peak and of the roofline, SQNR, end-to-end us (eager
+             qflash.forward, and one replay of it captured in a HIP graph)
 
 Timing: `--settle-ms` of back-to-back launches first (the clocks reach their
 loaded state), then W warmup launches, then K timed ones.
@@ -248,13 +249,15 @@ def run_config(name: str, steps: int, warmup: int, dev, seed: int = 0, cpu: bool
     res["roofline_frac"] = res["roofline_us"] / (ev_mean_ms * 1e3)
     if e2e:
         res["e2e_us"] = e2e_us(w, dev)
+        res["e2e_graph_us"] = e2e_graph_us(w, dev)
     if cpu:
         res["cpu_baseline"] = cpu_baseline(w, host_cores())
     return res
 
 
 PER_CONFIG_KEYS = ("config", "seed", "us_per_call", "us_per_call_median", "us_per_call_flushed", "kernel_tops",
-                   "mfma_frac", "roofline_us", "roofline_frac", "sqnr_db", "hbm_gbs_algorithmic", "e2e_us")
+                   "mfma_frac", "roofline_us", "roofline_frac", "sqnr_db", "hbm_gbs_algorithmic", "e2e_us",
+                   "e2e_graph_us")
 
 
 def per_config(dev, head=None, seeds=(0, 1, 2)):
@@ -304,6 +307,36 @@ def e2e_call(w, dev):
         def call():
             return qflash.forward(q, k, v, attn_mask=mask)
     return call
+
+
+def e2e_graph_us(w, dev, reps: int = 20) -> float:
+    """Median time of one replay of e2e_call captured in a HIP graph (HIP events
+    around each replay): the whole op with no host work between its kernels,
+    possible because the constants are formed on the device."""
+    import torch
+
+    call = e2e_call(w, dev)
+    call()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        call()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    for i in range(reps):
+        starts[i].record()
+        graph.replay()
+        ends[i].record()
+    torch.cuda.synchronize()
+    return statistics.median(a.elapsed_time(b) for a, b in zip(starts, ends)) * 1e3
 
 
 def e2e_us(w, dev, reps: int = 10) -> float:
@@ -421,6 +454,7 @@ def main(argv=None):
         "us_per_call_median": head["us_per_call_median"],
         "us_per_call_flushed": head["us_per_call_flushed"],
         "e2e_us": head["e2e_us"],
+        "e2e_graph_us": head["e2e_graph_us"],
         "sqnr_db": head["sqnr_db"],
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_INT8_TOPS, "unit": "TOPS",
                      "frac": achieved / PEAK_INT8_TOPS, "traffic": traffic,
