@@ -202,10 +202,11 @@ int qflash_hip_forward(const int8_t* Q, const int8_t* K, const int8_t* V, void* 
  * QFLASH_HIP_STATUS_* -- the first exception the reference's host raises on
  * the same value, in its order of evaluation (then no attention kernel reads
  * the constants and the outputs are left unwritten); [1..5] sm_rscale, exp_M,
- * req_M, l_M, acc_M; [6..12] the fast kernel's plan for N_CTX, HEAD_DIM and
- * masking; [14..15] sm_scale as a double.  Asynchronous on `stream`.
+ * req_M, l_M, acc_M; [6..12] and [16..18] the fast kernel's plan for N_CTX,
+ * HEAD_DIM and masking; [14..15] sm_scale as a double.  Asynchronous on
+ * `stream`.
  */
-#define QFLASH_HIP_PARAMS_WORDS 16
+#define QFLASH_HIP_PARAMS_WORDS 20
 #define QFLASH_HIP_STATUS_ZERODIV_SCALE 1   /* sm_scale == 0: ZeroDivisionError (1.0 / sm_scale) */
 #define QFLASH_HIP_STATUS_NAN 2             /* ValueError: cannot convert float NaN to integer */
 #define QFLASH_HIP_STATUS_INF 3             /* OverflowError: cannot convert float infinity to integer */
@@ -247,6 +248,17 @@ int qflash_hip_mfma_layout_check(const int8_t* A, const int8_t* B, int32_t* C, v
  * Host-only, needs no GPU.
  */
 int qflash_hip_lut_bounds(int32_t sm_rscale, int32_t exp_M, int32_t req_M, int32_t* lut_n, int32_t* lut_lim);
+
+/*
+ * Diagnostic, no counterpart in the reference: the range [u_lo, u_hi] of
+ * u = m' - s over which the masked fast kernel's table reads one constant
+ * p_far = int8(requant(exp2(-u))) (qflash/kernel.py:40-64) for the columns of
+ * a step whose biased score is negative (a -2^20 mask, padding), for the
+ * constants of a launch that has a table (lut_n > 0).  u_hi < u_lo: no such
+ * range.  Host-only, no GPU needed.
+ */
+int qflash_hip_far_bounds(int32_t sm_rscale, int32_t exp_M, int32_t req_M, int32_t* u_lo, int32_t* u_hi,
+                          int32_t* p_far);
 
 /*
  * Test hooks, no counterpart in the reference: each bit forces one of the

@@ -35,8 +35,8 @@ EXPORTS = ("qflash_hip_kernel", "qflash_hip_masked_kernel", "qflash_hip_window_k
            "qflash_hip_quantize", "qflash_hip_window_bias", "qflash_hip_mask_bias", "qflash_hip_constants",
            "qflash_hip_forward_planned", "qflash_hip_window_bias_planned", "qflash_hip_mask_bias_planned",
            "qflash_hip_last_error",
-           "qflash_hip_mfma_layout_check", "qflash_hip_lut_bounds", "qflash_hip_set_test_hooks",
-           "qflash_hip_version")
+           "qflash_hip_mfma_layout_check", "qflash_hip_lut_bounds", "qflash_hip_far_bounds",
+           "qflash_hip_set_test_hooks", "qflash_hip_version")
 
 # test-hook bits of qflash_hip_set_test_hooks (include/qflash_hip.h)
 HOOKS = {"FORCE_GENERAL": 1, "FORCE_DYNAMIC_BOUND": 2, "FORCE_ROBUST": 4, "NO_LUT": 8, "FORCE_LUT": 16}
@@ -45,7 +45,7 @@ HOOKS = {"FORCE_GENERAL": 1, "FORCE_DYNAMIC_BOUND": 2, "FORCE_ROBUST": 4, "NO_LU
 F32, F16, BF16, I8 = 0, 1, 2, 3
 SCALES_WORKSPACE = 256
 # device parameter block of qflash_hip_constants and its status codes
-PARAMS_WORDS = 16
+PARAMS_WORDS = 20
 STATUS_ZERODIV_SCALE, STATUS_NAN, STATUS_INF, STATUS_ZERODIV_RSCALE, STATUS_RANGE = 1, 2, 3, 4, 5
 
 E_HEADDIM = -2
@@ -92,6 +92,8 @@ def _declare(L):
     L.qflash_hip_mfma_layout_check.argtypes = [vp, vp, vp, vp]
     L.qflash_hip_lut_bounds.restype = ctypes.c_int
     L.qflash_hip_lut_bounds.argtypes = [i32, i32, i32, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]
+    L.qflash_hip_far_bounds.restype = ctypes.c_int
+    L.qflash_hip_far_bounds.argtypes = [i32, i32, i32] + [ctypes.POINTER(ctypes.c_int32)] * 3
     L.qflash_hip_set_test_hooks.restype = ctypes.c_uint32
     L.qflash_hip_set_test_hooks.argtypes = [ctypes.c_uint32]
     L.qflash_hip_version.restype = ctypes.c_char_p

@@ -84,6 +84,10 @@ struct Args {
     // for u = m' - s in [0, lut_lim], the table holding p(0 .. lut_n - 1) in reverse
     int32_t lut_n;      // table entries (the last one 0), 0 = no table
     int32_t lut_lim;
+    // masked table path: columns whose biased score is negative ("far" ones,
+    // such as those of a -2^20 mask) read entry lut_n = far_p, which is p(u)
+    // for every u in [far_lo + 1, far_hi] (far_bounds); far_hi = 0: no such range
+    int32_t far_lo, far_hi, far_p;
     // output: int8 codes at `o` (out_dt == QFLASH_HIP_I8), or RN_T(code * o_scale)
     // of type out_dt at the same element offsets of `out_t` (qflash/kernel.py:351)
     void* out_t;
@@ -98,8 +102,10 @@ struct Args {
 // Words of the device parameter block written by qflash_hip_constants.
 enum ParamWord : int {
     kPStatus = 0, kPRs, kPEm, kPRm, kPLm, kPAm, kPFast, kPIdOk, kPXSafe, kPEpsAbs, kPEAcc, kPLutN, kPLutLim,
-    kPSmScale = 14  // double, words 14-15
+    kPSmScale = 14,  // double, words 14-15
+    kPFarLo = 16, kPFarHi, kPFarP
 };
+static_assert(kPFarP < QFLASH_HIP_PARAMS_WORDS, "parameter block size");
 
 // The constants and plan fields of `a` from its device parameter block.
 __device__ __forceinline__ void load_params(Args& a) {
@@ -115,6 +121,9 @@ __device__ __forceinline__ void load_params(Args& a) {
     a.e_acc = p[kPEAcc];
     a.lut_n = p[kPLutN];
     a.lut_lim = p[kPLutLim];
+    a.far_lo = p[kPFarLo];
+    a.far_hi = p[kPFarHi];
+    a.far_p = p[kPFarP];
 }
 
 __device__ __forceinline__ int out_esize(int dt) { return dt == QFLASH_HIP_I8 ? 1 : (dt == QFLASH_HIP_F32 ? 4 : 2); }
@@ -894,36 +903,59 @@ __device__ __forceinline__ int32_t min_first(const i32x16& s) {
     if constexpr (TV > 2 && TV % 2) m = min(m, s[TV - 1]);
     return m;
 }
+template <int TV>
+__device__ __forceinline__ uint32_t umin_first(const i32x16& s) {
+    uint32_t m = TV == 1 ? (uint32_t)s[0] : min((uint32_t)s[0], (uint32_t)s[1]);
+#pragma unroll
+    for (int v = 2; v + 1 < TV; v += 2) m = min(min(m, (uint32_t)s[v]), (uint32_t)s[v + 1]);
+    if constexpr (TV > 2 && TV % 2) m = min(m, (uint32_t)s[TV - 1]);
+    return m;
+}
 
 // S^T tile of one step with bias and padding applied (kernel.py:153-156, :250-253);
 // returns the row max over the 32 columns (both lane halves).
-// smin: the minimum over the real columns when MASKED or need_min (else INT32_MAX).
-// Unmasked: every score carries kScoreBias, from an extra MFMA of xb (all
-// bytes -128) with itself.  TV < 16 (partial steps of at most 2*TV keys):
-// registers TV..15 hold padded columns only and are set to the padding value.
+// Every score carries kScoreBias, from an extra MFMA of xb (all bytes -128)
+// with itself (int32 arithmetic wraps, so differences are unchanged).
+// smin: the minimum over the real columns when MASKED or need_min (else
+// INT32_MAX); sminu (MASKED): their minimum as unsigned values, i.e. over the
+// columns whose biased score is non-negative (else UINT32_MAX).
+// TV < 16 (partial steps of at most 2*TV keys): registers TV..15 hold padded
+// columns only and are set to the padding value.
 template <int D, bool MASKED, bool TAIL, int TV = 16>
-__device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& a, const i32x4* qv,
-                                          const int8_t* lk, const Frag<D>& fr, const int32_t* bias_v, int kstart,
-                                          int lane, bool need_min, i32x4 xb) {
+__device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, uint32_t& sminu, const Args& a,
+                                          const i32x4* qv, const int8_t* lk, const Frag<D>& fr,
+                                          const int32_t* bias_v, int kstart, int lane, bool need_min, i32x4 xb) {
     constexpr int DB = D / 32;
-    constexpr int32_t PAD = kNegInf + (MASKED ? 0 : kScoreBias);
+    constexpr int32_t PAD = kNegInf + kScoreBias;
     // K fragments first: the bias MFMA runs while they are in flight
     i32x4 kf[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db) kf[db] = *reinterpret_cast<const i32x4*>(lk + fr.k[db]);
-    if constexpr (MASKED)
-        s = i32x16{};
-    else
+    if constexpr (MASKED) {
+        // the bias enters as the accumulator of the first MFMA (int32 sums wrap)
+        i32x16 c;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) c[v] = bias_v[v];
+        s = mfma32(xb, xb, c);
+    } else {
         s = mfma32(xb, xb, i32x16{});
+    }
 #pragma unroll
     for (int db = 0; db < DB; ++db) s = mfma32(kf[db], qv[db], s);
     smin = INT32_MAX;
+    sminu = UINT32_MAX;
     const int32_t tcut = a.N - kstart - 4 * (lane >> 5);
     if constexpr (MASKED) {
+        if constexpr (!TAIL) {
+            smin = min_first<TV>(s);
+            sminu = umin_first<TV>(s);
+        } else {
 #pragma unroll
-        for (int v = 0; v < TV; ++v) {
-            s[v] = wadd(s[v], bias_v[v]);
-            if (!TAIL || !padded(v, tcut)) smin = min(smin, s[v]);
+            for (int v = 0; v < TV; ++v)
+                if (!padded(v, tcut)) {
+                    smin = min(smin, s[v]);
+                    sminu = min(sminu, (uint32_t)s[v]);
+                }
         }
     } else if (need_min) {
         // over the raw scores: a padded column's raw score (its K row reads as
@@ -942,14 +974,17 @@ __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, const Args& 
 // One 32-key step (qflash/kernel.py:147-174) for the 32 query rows of a wave.
 // Every branch below is wave-uniform and none of them holds an alternative
 // computation of acc (the accumulators keep their registers across steps).
-// Scores, m and m' carry the bias SB (kScoreBias when unmasked): only their
-// differences enter the arithmetic.  LUT: LDS address of the p table.
+// Scores, m and m' carry the bias SB = kScoreBias: only their differences
+// (wrapping, as the reference's int32 arithmetic) enter the arithmetic, and
+// the running maximum is the reference's one plus SB as long as no biased
+// value wraps (checked for masked steps; unmasked scores are bounded by
+// 128 * ||q||_1).  LUT: LDS address of the p table.
 template <int D, int LUT, bool MASKED, bool TAIL, bool WIDE, bool DYN, bool FIRST, int TV = 16>
 __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const i32x4* qv, const int8_t* lk,
                                           const int8_t* lv, const Frag<D>& fr, const BiasRow& brow, int kstart,
                                           int lane, bool wave_fast, int32_t xlim, int lut_mode, i32x4 xb) {
     constexpr int DB = D / 32;
-    constexpr int32_t SB = MASKED ? 0 : kScoreBias;
+    constexpr int32_t SB = kScoreBias;
     const int g = lane >> 5;
     const int32_t rs = a.rs, eM = a.eM, rM = a.rM;
 
@@ -957,36 +992,62 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     if constexpr (MASKED) load_bias<TAIL>(bias_v, a, brow, kstart, lane);
     i32x16 s;
     int32_t smin;
+    uint32_t sminu;
     static_assert(TV == 16 || (TAIL && (TV == 4 || TV == 8 || TV == 12)), "TV < 16: partial steps of <= 2*TV keys");
-    const int32_t mx = scores<D, MASKED, TAIL, TV>(s, smin, a, qv, lk, fr, bias_v, kstart, lane, lut_mode == 2, xb);
+    const int32_t mx =
+        scores<D, MASKED, TAIL, TV>(s, smin, sminu, a, qv, lk, fr, bias_v, kstart, lane, lut_mode == 2, xb);
     const int32_t m = st.m;
-    const int32_t mn = max(m, mx);  // kernel.py:158
-    const int32_t dm = wsub(m, mn);
+    int32_t mn = max(m, mx);  // kernel.py:158
     constexpr bool first = FIRST;  // kstart == 0
 
-    // Each lane half checks its own minimum against the row's mn (the checks
-    // below are wave-wide); a masked partial step's half may have no real
-    // column (minimum INT32_MAX) and takes the other half's.
-    if constexpr (MASKED && TAIL) smin = half_min(smin);
-    // table path: every real column of the wave has u = m' - s <= lut_lim
-    // (lut_mode 1: proved for the whole row block from ||q||_1)
-    // (mn >= smin: the difference is exact as an unsigned 32-bit value)
-    const bool lut_ok = lut_mode == 1 || (lut_mode == 2 && __all((uint32_t)(mn - smin) <= (uint32_t)a.lut_lim));
-    bool vec_ok = wave_fast;
-    if constexpr (MASKED)
-        vec_ok = vec_ok && __all(smin > -(1 << 23) && mn < (1 << 23) && (int64_t)mn - smin <= xlim);
+    // Table path.  Unmasked: every real column of the wave has u = m' - s <=
+    // lut_lim (lut_mode 1: proved for the whole row block from ||q||_1; the
+    // difference is exact as an unsigned 32-bit value since m' >= s).
+    // Masked: the columns split by the sign of the biased score s'.  Those with
+    // s' >= 0 need u <= lut_lim (checked on their minimum, sminu, or on m'
+    // itself when there is none); those with s' < 0 have u = m' - s' >= m' + 1
+    // >= far_lo + 1 and need u <= far_hi, where p is the constant far_p
+    // (far_bounds); far_lo >= lut_n - 1 keeps thr below non-negative.  The far
+    // check runs on min(smin, m): a wrapped biased value (below INT32_MIN + SB,
+    // from a reference score >= 2^31 - SB) in this step or in m, the only case
+    // in which m' is not the reference's maximum plus SB, fails it (far_hi <=
+    // 2^30) and the 24-bit range check below.  A partial step's half with no
+    // real column has smin = INT32_MAX, sminu = UINT32_MAX.  The conditions are
+    // combined without short-circuit branches.
+    bool lut_ok;
+    int32_t slo = smin;
+    if constexpr (MASKED) {
+        slo = min(smin, m);
+        const bool far_ok = (mn >= a.far_lo) & ((uint32_t)(mn - slo) <= (uint32_t)a.far_hi);
+        const bool near_ok = (uint32_t)mn - min(sminu, (uint32_t)mn) <= (uint32_t)a.lut_lim;
+        lut_ok = lut_mode == 2 && __all(far_ok & near_ok);
+    } else {
+        lut_ok = lut_mode == 1 || (lut_mode == 2 && __all((uint32_t)(mn - smin) <= (uint32_t)a.lut_lim));
+    }
+    // 24-bit arithmetic path: masked steps check |x| <= xlim and the 24-bit
+    // operand range (then mn - slo < 2^24 is exact in int32), evaluated only
+    // when the table path is not taken
+    auto vec_ok = [&]() {
+        if constexpr (MASKED)
+            return wave_fast && __all((slo > -(1 << 23)) & (mn < (1 << 23)) & (wsub(mn, slo) <= xlim));
+        else
+            return wave_fast;
+    };
     uint32_t pk[4];
     i32x4 vf[DB];
     if (lut_ok) {
-        // table index max(s - thr, 0) = lut_n - 1 - min(u, lut_n - 1)
+        // table index max(s - thr, 0) = lut_n - 1 - min(u, lut_n - 1) with one
+        // unsigned saturating subtraction: thr in [0, 2^31) and, for the
+        // columns it serves, s in [0, 2^31) (unmasked: s >= SB - 128 * ||q||_1
+        // > lut_n - 1, lut_mode != 0 only then)
         const int32_t thr = wsub(mn, a.lut_n - 1);
         uint32_t idx[16];
         if constexpr (MASKED) {
-            // real columns: s - thr = lut_n - 1 - u >= lut_n - 1 - lut_lim > INT32_MIN, no wrap
+            // s' < 0 reads as >= 2^31 > thr + lut_n - 1: clamped to entry lut_n = far_p
 #pragma unroll
-            for (int v = 0; v < TV; ++v) idx[v] = (uint32_t)max(wsub(s[v], thr), 0);
+            for (int v = 0; v < TV; ++v)
+                idx[v] = min(__builtin_elementwise_sub_sat((uint32_t)s[v], (uint32_t)thr), (uint32_t)a.lut_n);
         } else {
-            // scores and thr in [1, 2^31) (lut_mode != 0 only then): unsigned saturation
 #pragma unroll
             for (int v = 0; v < TV; ++v) idx[v] = __builtin_elementwise_sub_sat((uint32_t)s[v], (uint32_t)thr);
         }
@@ -1000,7 +1061,7 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
             lut_pack_vtn<D, LUT, TV>(pk, vf, idx, lv, fr);
         else
             lut_pack_vt<D, LUT>(pk, vf, idx, lv, fr);
-    } else if (vec_ok) {
+    } else if (vec_ok()) {
         // kernel.py:159-161 in six ops per score (see the fast-path comment)
         const int32_t c1 = opaque(wadd(wmul(wsub(0, mn), eM), 1 << 16));
         const int32_t c3 = opaque(wsub(rs, mn));
@@ -1027,6 +1088,15 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
             pk[w4] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
         }
     } else {  // general exact arithmetic for this step's scores (p in bits 0-7)
+        if constexpr (MASKED) {
+            // a wrapped biased value: the maximum over the reference's values
+            if (__builtin_expect(__any(slo < INT32_MIN + SB), 0)) {
+                int32_t r = wsub(s[0], SB);
+#pragma unroll
+                for (int v = 1; v < 16; ++v) r = max(r, wsub(s[v], SB));
+                mn = wadd(max(wsub(m, SB), half_max(r)), SB);
+            }
+        }
         // One score at a time through a rotating queue: this rare path then holds
         // the temporaries of one evaluation only, not of sixteen interleaved ones.
 #pragma unroll 1
@@ -1056,6 +1126,7 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
         if (lut_ok) lij = wadd(lij, (32 - (a.N - kstart)) * requant(exp2_i32(wsub(kNegInf + SB, mn), a), a));
     }
 
+    const int32_t dm = wsub(m, mn);
     // kernel.py:163-165
     int32_t alpha;
     bool wide_step;
@@ -1177,39 +1248,47 @@ __device__ __forceinline__ void fast_store(const FastState<D>& st, const Args& a
                                            double* yslot) {
     constexpr int DB = D / 32;
     const int lq = lane & 31, g = lane >> 5;
-    const float b_row = (float)st.l;            // S layout: lane = row
-    const double y_row = 1.0 / (double)b_row;
+    const float b_row = (float)st.l;  // S layout: lane = row
     const bool exact = __any(st.l >= -1 && st.l <= 1);
-    // y of the 32 rows to LDS (this wave's 256 bytes), read back two rows at a
-    // time in the O layout (rows 8(v>>2) + 4g + (v&3), v and v+1 adjacent):
-    // 8 broadcast reads instead of 32 lane permutes
-    if (!exact && g == 0) yslot[lq] = y_row;
     const int32_t so2 = (int32_t)a.so[2];
     const __amdgpu_buffer_rsrc_t rsrc = out_rsrc(a, z, h, D);
     const float os = a.out_dt == QFLASH_HIP_I8 ? 0.f : scale_value(a);
     const int32_t voff = (q0 + 4 * g) * so2 + lq;
-    with_out_type(a.out_dt, [&]<int OUT>() {
+    if (!exact) {
+        // y of the 32 rows to LDS (this wave's 256 bytes, 16-byte aligned), read
+        // back two rows at a time in the O layout (registers v and v+1, v even,
+        // hold rows r and r+1 of this lane half)
+        if (g == 0) yslot[lq] = 1.0 / (double)b_row;
+        with_out_type(a.out_dt, [&]<int OUT>() {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int row = crow(v, lane);
-            const int32_t soff = (8 * (v >> 2) + (v & 3)) * so2;
-            if (!exact) {
-                const double yd = yslot[row];
+            for (int v = 0; v < 16; v += 2) {
+                typedef double f64x2 __attribute__((ext_vector_type(2)));
+                const f64x2 y2 = *reinterpret_cast<const f64x2*>(yslot + crow(v, lane));
 #pragma unroll
-                for (int t = 0; t < DB; ++t) {
-                    const float qf = (float)((double)(float)st.acc[t][v] * yd);
-                    put_out<OUT>(rsrc, (int32_t)qf, voff + t * 32, soff, os);
+                for (int j = 0; j < 2; ++j) {
+                    const int32_t soff = (8 * ((v + j) >> 2) + ((v + j) & 3)) * so2;
+#pragma unroll
+                    for (int t = 0; t < DB; ++t) {
+                        const float qf = (float)((double)(float)st.acc[t][v + j] * y2[j]);
+                        put_out<OUT>(rsrc, (int32_t)qf, voff + t * 32, soff, os);
+                    }
                 }
-            } else {
-                const float bf = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * row, __float_as_int(b_row)));
+            }
+        });
+    } else {
+        with_out_type(a.out_dt, [&]<int OUT>() {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int32_t soff = (8 * (v >> 2) + (v & 3)) * so2;
+                const float bf = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * crow(v, lane), __float_as_int(b_row)));
 #pragma unroll
                 for (int t = 0; t < DB; ++t) {
                     const int32_t code = cvt_x86(__fdiv_rn((float)st.acc[t][v], bf));
                     put_out<OUT>(rsrc, code, voff + t * 32, soff, os);
                 }
             }
-        }
-    });
+        });
+    }
 }
 
 // The 32 query rows of one wave: K / V stages double-buffered in LDS (the
@@ -1228,8 +1307,8 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
     FastState<D> st;
 #pragma unroll
     for (int t = 0; t < DB; ++t) st.acc[t] = i32x16{};
-    st.m = kNegInf + (MASKED ? 0 : kScoreBias);  // kernel.py:138
-    st.l = 1;                                     // kernel.py:139
+    st.m = kNegInf + kScoreBias;  // kernel.py:138
+    st.l = 1;                     // kernel.py:139
     st.bnd = 0.f;
     st.wide = 0;
     // all bytes -128; opaque to the compiler each step, so that the bias MFMA
@@ -1264,7 +1343,7 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
                 const int step = stg * S::STEPS + half;
                 if (half == 0 && stg == 0) continue;  // step 0 ran above
                 if (step >= nfull) break;
-                if constexpr (!MASKED) asm volatile("" : "+v"(xb));
+                if constexpr (!MASKED) asm volatile("" : "+v"(xb));  // masked: C = bias, not hoistable
                 fast_step<D, LUT, MASKED, false, WIDE, DYN, false>(st, a, qv, buf + half * 32 * D,
                                                                    buf + S::KBYTES + half * 32 * D, fr, brow,
                                                                    step * 32, lane, wave_fast, xlim, lut_mode, xb);
@@ -1392,15 +1471,23 @@ __device__ __forceinline__ void fast_block(const Args& a, int8_t* smem, int zh, 
     }
 }
 
+// The p(u) table at lut, entry lut_n - 1 - u (lut_pack_vt), and for masked
+// launches the far columns' constant at entry lut_n (lut_n + 1 <= kLutMax,
+// host); visible after fast_rows' first barrier.  lut_n - 1 <= x_safe (host),
+// where the 24-bit E is exact.
+template <int W, bool MASKED>
+__device__ __forceinline__ void fill_lut(const Args& a, int8_t* lut) {
+    for (int u = threadIdx.x; u < a.lut_n; u += 64 * W)
+        lut[a.lut_n - 1 - u] = (int8_t)(mad24(exp2_fast(-u, a.eM, a.rs), a.rM, 1 << 15) >> 16);
+    if constexpr (MASKED)
+        if (threadIdx.x == 0 && a.lut_n > 0) lut[a.lut_n] = (int8_t)a.far_p;
+}
+
 template <int D, int W, bool MASKED, bool DYN>
 __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Args a) {
     using S = Stage<D, W>;
     __shared__ __attribute__((aligned(16))) int8_t smem[2 * S::BYTES + kLutMax];
-    // p(u) table, entry lut_n - 1 - u (lut_pack_vt), visible after fast_rows'
-    // first barrier; lut_n - 1 <= x_safe (host), where the 24-bit E is exact
-    for (int u = threadIdx.x; u < a.lut_n; u += 64 * W)
-        smem[2 * S::BYTES + a.lut_n - 1 - u] =
-            (int8_t)(mad24(exp2_fast(-u, a.eM, a.rs), a.rM, 1 << 15) >> 16);
+    fill_lut<W, MASKED>(a, smem + 2 * S::BYTES);
     const int wg = xcd_order(blockIdx.x, a.n_wg);
     fast_block<D, W, MASKED, DYN>(a, smem, wg / a.mblocks, wg % a.mblocks);
 }
@@ -1420,9 +1507,7 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast_pla
         general_block<D, W, MASKED, true>(a, xcd_order(blockIdx.x, a.n_wg), smem);
         return;
     }
-    for (int u = threadIdx.x; u < a.lut_n; u += 64 * W)
-        smem[2 * S::BYTES + a.lut_n - 1 - u] =
-            (int8_t)(mad24(exp2_fast(-u, a.eM, a.rs), a.rM, 1 << 15) >> 16);
+    fill_lut<W, MASKED>(a, smem + 2 * S::BYTES);
     const int wg = xcd_order(blockIdx.x, a.n_wg);
     if (a.id_ok)
         fast_block<D, W, MASKED, false>(a, smem, wg / a.mblocks, wg % a.mblocks);

@@ -84,7 +84,8 @@ __host__ __device__ static int64_t lut_range(const Args& a, int64_t* lim_out) {
     int bl = 0;
     while ((1ll << bl) <= rs) ++bl;
     const int64_t u0 = ((bl + 3) * 65536 + A - 1) / A;  // q >= bitlen(rs) + 3 for u >= u0
-    if (u0 > lim || u0 >= kLutMax) return -1;
+    // lut_n <= u0 + 1 entries, and the masked kernels' far entry after them
+    if (u0 > lim || u0 >= kLutMax - 1) return -1;
     *lim_out = lim;
     return u0;
 }
@@ -105,6 +106,50 @@ static void lut_bounds(const Args& a, int32_t* n_out, int32_t* lim_out) {
     *lim_out = (int32_t)lim;
 }
 
+// Far columns of the masked table path.  For u = m' - s >= 0 with u*|eM| < 2^31
+// (u <= hi) write u*|eM| = 2^16 q + f, 0 <= f < 2^16; then exp2's remainder is
+// r = q*rs - u = (u*kappa - rs*f) / 2^16 (kappa = |eM|*rs - 2^16), and for
+// q >= 32 (u >= ceil(2^21 / |eM|)) E = ((r >> 1) + rs) >> q is the sign fill
+// of (r >> 1) + rs:
+//   kappa >= 0: r > -rs, so (r >> 1) + rs >= rs/2 > 0: E = 0, p = 0;
+//   kappa <  0: r <= -u*|kappa| / 2^16 < -2 rs once u > 2 rs 2^16 / |kappa|,
+//               so (r >> 1) + rs <= -1: E = -1, p = requant(-1).
+// Over u in [lo, hi] p is that one constant.  The kernel reads it for every
+// column whose biased score s' = s + kScoreBias is negative once a step has
+// m' >= far_lo = max(lo - 1, lut_n - 1) (then u = m' - s' >= lo) and
+// m' - min s' <= far_hi = min(hi, 2^30) (2^30 also rejects a wrapped s').
+// u_lo / u_hi / p_far: the range and the constant (u_hi < u_lo: none).
+__host__ __device__ static void far_range(const Args& a, int64_t* u_lo, int64_t* u_hi, int32_t* p_far) {
+    *u_lo = 1;
+    *u_hi = 0;
+    *p_far = 0;
+    const int64_t A = -(int64_t)a.eM, rs = a.rs;
+    if (!a.exp_mode || A <= 0 || rs <= 0) return;
+    const int64_t kap = A * rs - 65536;
+    int64_t lo = ((int64_t)32 * 65536 + A - 1) / A;
+    if (kap < 0 && 2 * rs * 65536 / -kap + 1 > lo) lo = 2 * rs * 65536 / -kap + 1;
+    int64_t hi = (int64_t)INT32_MAX / A;
+    if (hi > (1 << 30)) hi = 1 << 30;
+    *u_lo = lo;
+    *u_hi = hi;
+    *p_far = kap < 0 ? requant(-1, a) : 0;
+}
+
+// The far-column fields of a masked launch with a table (a.lut_n > 0).
+__host__ __device__ static void far_bounds(Args& a) {
+    a.far_lo = a.lut_n > 0 ? a.lut_n - 1 : 0;
+    a.far_hi = 0;
+    a.far_p = 0;
+    if (a.lut_n <= 0) return;
+    int64_t lo, hi;
+    int32_t p;
+    far_range(a, &lo, &hi, &p);
+    if (lo > hi) return;
+    if (lo - 1 > a.far_lo) a.far_lo = (int32_t)(lo - 1);
+    a.far_hi = (int32_t)hi;
+    a.far_p = p;
+}
+
 // Whether the table pays for this launch (test hooks aside): filling it costs
 // each workgroup a few hundred VALU operations and every step an LDS round
 // trip; it replaces ~80 VALU instructions per 32-key step, and filling it
@@ -116,16 +161,17 @@ __host__ __device__ static bool lut_wanted(const Args& a, bool no_lut, bool forc
 }
 
 // The table for this call, or none (lut_n = 0).
-static void choose_lut(Args& a, int W) {
+static void choose_lut(Args& a, bool masked) {
     a.lut_n = 0;
     a.lut_lim = 0;
-    (void)W;
+    a.far_lo = a.far_hi = a.far_p = 0;
     if (!lut_wanted(a, hook(QFLASH_HIP_HOOK_NO_LUT), hook(QFLASH_HIP_HOOK_FORCE_LUT))) return;
     int32_t n, lim;
     lut_bounds(a, &n, &lim);
     if (n - 1 > a.x_safe) return;  // the kernel fills the table with the 24-bit E
     a.lut_n = n;
     a.lut_lim = lim;
+    if (masked) far_bounds(a);
 }
 
 // Proof obligations of fwd_fast on the constants (see the comment above it).
@@ -228,6 +274,7 @@ __global__ __launch_bounds__(64) void constants_kernel(const void* scales, int32
     const int status = device_constants(sm, a.l_shift, a.acc_shift, c);
     a.rs = c[0]; a.eM = c[1]; a.rM = c[2]; a.lM = c[3]; a.aM = c[4];
     a.id_ok = a.x_safe = a.eps_abs = a.e_acc = a.lut_n = a.lut_lim = 0;
+    a.far_lo = a.far_hi = a.far_p = 0;
     bool fast = false;
     if (status == 0) {
         fast = !(hooks & QFLASH_HIP_HOOK_FORCE_GENERAL) && fast_consts(a, masked != 0);
@@ -246,13 +293,15 @@ __global__ __launch_bounds__(64) void constants_kernel(const void* scales, int32
             if (u0 >= 0 && n - 1 <= a.x_safe) {
                 a.lut_n = (int32_t)n;
                 a.lut_lim = (int32_t)lim;
+                if (masked) far_bounds(a);
             }
         }
         if (hooks & QFLASH_HIP_HOOK_FORCE_DYNAMIC_BOUND) a.id_ok = 0;
     }
     if (lane == 0) {
-        int32_t w[16] = {status, a.rs, a.eM, a.rM, a.lM, a.aM, fast ? 1 : 0, a.id_ok, a.x_safe, a.eps_abs, a.e_acc,
-                         a.lut_n, a.lut_lim, 0, 0, 0};
+        int32_t w[QFLASH_HIP_PARAMS_WORDS] = {status, a.rs, a.eM, a.rM, a.lM, a.aM, fast ? 1 : 0, a.id_ok, a.x_safe,
+                                              a.eps_abs, a.e_acc, a.lut_n, a.lut_lim, 0, 0, 0, a.far_lo, a.far_hi,
+                                              a.far_p, 0};
         const uint64_t smb = __double_as_longlong(sm);
         w[kPSmScale] = (int32_t)(uint32_t)smb;
         w[kPSmScale + 1] = (int32_t)(uint32_t)(smb >> 32);
@@ -347,7 +396,7 @@ static int forward(const int8_t* Q, const int8_t* K, const int8_t* V, void* O, c
         a.general_only = fast ? 0 : 1;
     } else {
         fast = choose_fast(a, D, masked, vec) && !hook(QFLASH_HIP_HOOK_FORCE_GENERAL);
-        if (fast) choose_lut(a, W);
+        if (fast) choose_lut(a, masked);
         if (hook(QFLASH_HIP_HOOK_FORCE_DYNAMIC_BOUND)) a.id_ok = 0;
     }
     dim3 grid((unsigned)nwg);
@@ -472,6 +521,22 @@ int qflash_hip_lut_bounds(int32_t sm_rscale, int32_t exp_M, int32_t req_M, int32
     a.rM = req_M;
     a.exp_mode = 1;
     qf::lut_bounds(a, lut_n, lut_lim);
+    return QFLASH_HIP_OK;
+}
+
+int qflash_hip_far_bounds(int32_t sm_rscale, int32_t exp_M, int32_t req_M, int32_t* u_lo, int32_t* u_hi,
+                          int32_t* p_far) {
+    qferr::g_err[0] = 0;
+    if (!u_lo || !u_hi || !p_far) return qferr::fail(QFLASH_HIP_EINVAL, "null pointer argument");
+    qf::Args a{};
+    a.rs = sm_rscale;
+    a.eM = exp_M;
+    a.rM = req_M;
+    a.exp_mode = 1;
+    int64_t lo, hi;
+    qf::far_range(a, &lo, &hi, p_far);
+    *u_lo = (int32_t)(lo < INT32_MAX ? lo : INT32_MAX);
+    *u_hi = (int32_t)hi;
     return QFLASH_HIP_OK;
 }
 

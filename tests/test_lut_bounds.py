@@ -98,3 +98,57 @@ def test_negative_kappa_limit_is_needed():
 
 def test_rejects_null_outputs(lib):
     assert lib.qflash_hip_lut_bounds(57, -1146, 145571, None, None) == -1  # QFLASH_HIP_EINVAL
+
+
+def _far(lib, c: Consts):
+    lo, hi, p = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    assert lib.qflash_hip_far_bounds(c.sm_rscale, c.exp_M, c.req_M, ctypes.byref(lo), ctypes.byref(hi),
+                                     ctypes.byref(p)) == 0
+    return lo.value, hi.value, p.value
+
+
+FAR_EDGE = 1 << 20       # brute-force span at each end of a far range
+
+
+@pytest.mark.parametrize("sm_scale", SCALES)
+def test_far_range_is_constant(lib, sm_scale):
+    """The masked table path gives every column with a negative biased score
+    the one value p_far, relying on p(u) = p_far for all u in [u_lo, u_hi]
+    (qflash_hip_far_bounds).  Checked by brute force over FAR_EDGE values at
+    each end of the range and 2^16 random ones between; the table itself
+    (lut_n > 0) is the precondition of the range's use."""
+    c = Consts(*fixed_point_constants(sm_scale, 30, 30))
+    n, _ = _bounds(lib, c)
+    lo, hi, p_far = _far(lib, c)
+    if n == 0 or hi < lo:
+        return
+    assert hi <= min((2 ** 31 - 1) // -c.exp_M, 2 ** 30)
+    rng = np.random.default_rng(int(sm_scale * 1e6))
+    us = np.unique(np.concatenate([np.arange(lo, min(hi, lo + FAR_EDGE) + 1),
+                                   np.arange(max(lo, hi - FAR_EDGE), hi + 1),
+                                   rng.integers(lo, hi + 1, 1 << 16)]))
+    p = _p(us, c)
+    bad = us[p != p_far]
+    assert bad.size == 0, f"p(u) != {p_far} at u = {bad[:5]}"
+
+
+def test_far_constant_takes_both_values():
+    """Across the sweep the far constant is 0 (kappa >= 0) and requant(-1) < 0
+    (kappa < 0), and the ranges of the Swin-like scales (sm_scale ~ 0.02-0.03)
+    reach -2^20 - 2^19 below a row maximum of 2^19 (biased)."""
+    lib = _lib.load()
+    vals, reach = set(), 0
+    for sm in SCALES:
+        c = Consts(*fixed_point_constants(sm, 30, 30))
+        n, _ = _bounds(lib, c)
+        lo, hi, p_far = _far(lib, c)
+        if n and hi >= lo:
+            vals.add(p_far < 0)
+            if 0.015 < sm < 0.035:
+                reach += lo <= (1 << 19) and hi >= (1 << 19) + (1 << 20) + (1 << 19)
+    assert vals == {True, False}
+    assert reach > 0
+
+
+def test_far_bounds_rejects_null_outputs(lib):
+    assert lib.qflash_hip_far_bounds(57, -1146, 145571, None, None, None) == -1
