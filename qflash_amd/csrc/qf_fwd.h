@@ -535,45 +535,46 @@ struct Frag {
 // per 32-column block, the second 16 keys (16*D bytes) further.  Written as
 // one asm block with its own lgkmcnt wait: through the builtin, the compiler
 // would also wait for the in-flight copy of the NEXT stage (vmcnt(0)) before
-// every read, as it cannot tell the two LDS buffers apart.
-template <int D>
-__device__ __forceinline__ void read_vt(i32x4* vf, const int8_t* lv, const Frag<D>& fr) {
+// every read, as it cannot tell the two LDS buffers apart.  The tile sits at
+// LDS address vbase + VO: the steps of the main loop pass the constant part
+// as the immediate VO (vbase is then the LDS array's own address, a
+// constant the compiler folds), so their reads need no address arithmetic.
+#define QF_TR32                                           \
+    "ds_read_b64_tr_b8 %[t0], %[b0] offset:%c[vo]\n\t"    \
+    "ds_read_b64_tr_b8 %[t1], %[b0] offset:%c[vo2]\n\t"
+#define QF_TR64 QF_TR32                                   \
+    "ds_read_b64_tr_b8 %[t2], %[b1] offset:%c[vo]\n\t"    \
+    "ds_read_b64_tr_b8 %[t3], %[b1] offset:%c[vo2]\n\t"
+#define QF_TR128 QF_TR64                                  \
+    "ds_read_b64_tr_b8 %[t4], %[b2] offset:%c[vo]\n\t"    \
+    "ds_read_b64_tr_b8 %[t5], %[b2] offset:%c[vo2]\n\t"   \
+    "ds_read_b64_tr_b8 %[t6], %[b3] offset:%c[vo]\n\t"    \
+    "ds_read_b64_tr_b8 %[t7], %[b3] offset:%c[vo2]\n\t"
+#define QF_T32 [t0] "=&v"(t[0]), [t1] "=&v"(t[1])
+#define QF_T64 QF_T32, [t2] "=&v"(t[2]), [t3] "=&v"(t[3])
+#define QF_T128 QF_T64, [t4] "=&v"(t[4]), [t5] "=&v"(t[5]), [t6] "=&v"(t[6]), [t7] "=&v"(t[7])
+#define QF_B32 [b0] "v"(vbase + fr.v[0]), [vo] "i"(VO), [vo2] "i"(VO + 16 * D)
+#define QF_B64 QF_B32, [b1] "v"(vbase + fr.v[1])
+#define QF_B128 QF_B64, [b2] "v"(vbase + fr.v[2]), [b3] "v"(vbase + fr.v[3])
+
+// LDS address of a shared-memory pointer
+__device__ __forceinline__ uint32_t lds_addr(const int8_t* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)p;
+}
+
+template <int D, int VO>
+__device__ __forceinline__ void read_vt(i32x4* vf, uint32_t vbase, const Frag<D>& fr) {
+    static_assert(VO >= 0 && VO + 16 * D < 65536, "offsets must fit the 16-bit LDS immediate");
     typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
-    const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)lv;
-    i32x2 r[2 * (D / 32)];
-    if constexpr (D == 32) {
-        asm volatile(
-            "ds_read_b64_tr_b8 %0, %2\n\t"
-            "ds_read_b64_tr_b8 %1, %2 offset:%c3\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=&v"(r[0]), "=&v"(r[1])
-            : "v"(base + fr.v[0]), "i"(16 * D));
-    } else if constexpr (D == 64) {
-        asm volatile(
-            "ds_read_b64_tr_b8 %0, %4\n\t"
-            "ds_read_b64_tr_b8 %1, %4 offset:%c6\n\t"
-            "ds_read_b64_tr_b8 %2, %5\n\t"
-            "ds_read_b64_tr_b8 %3, %5 offset:%c6\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
-            : "v"(base + fr.v[0]), "v"(base + fr.v[1]), "i"(16 * D));
-    } else {
-        asm volatile(
-            "ds_read_b64_tr_b8 %0, %8\n\t"
-            "ds_read_b64_tr_b8 %1, %8 offset:%c12\n\t"
-            "ds_read_b64_tr_b8 %2, %9\n\t"
-            "ds_read_b64_tr_b8 %3, %9 offset:%c12\n\t"
-            "ds_read_b64_tr_b8 %4, %10\n\t"
-            "ds_read_b64_tr_b8 %5, %10 offset:%c12\n\t"
-            "ds_read_b64_tr_b8 %6, %11\n\t"
-            "ds_read_b64_tr_b8 %7, %11 offset:%c12\n\t"
-            "s_waitcnt lgkmcnt(0)"
-            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]),
-              "=&v"(r[7])
-            : "v"(base + fr.v[0]), "v"(base + fr.v[1]), "v"(base + fr.v[2]), "v"(base + fr.v[3]), "i"(16 * D));
-    }
+    i32x2 t[2 * (D / 32)];
+    if constexpr (D == 32)
+        asm volatile(QF_TR32 "s_waitcnt lgkmcnt(0)" : QF_T32 : QF_B32);
+    else if constexpr (D == 64)
+        asm volatile(QF_TR64 "s_waitcnt lgkmcnt(0)" : QF_T64 : QF_B64);
+    else
+        asm volatile(QF_TR128 "s_waitcnt lgkmcnt(0)" : QF_T128 : QF_B128);
 #pragma unroll
-    for (int t = 0; t < D / 32; ++t) vf[t] = i32x4{r[2 * t].x, r[2 * t].y, r[2 * t + 1].x, r[2 * t + 1].y};
+    for (int i = 0; i < D / 32; ++i) vf[i] = i32x4{t[2 * i].x, t[2 * i].y, t[2 * i + 1].x, t[2 * i + 1].y};
 }
 
 // Direct HBM -> LDS copies of one stage: slot s of a tile (16 bytes at byte
@@ -628,6 +629,11 @@ __device__ __forceinline__ int32_t half_max(int32_t v) {
     const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
     return max((int32_t)r[0], (int32_t)r[1]);
 }
+// max(v, v of lane ^ 32, c)
+__device__ __forceinline__ int32_t half_max3(int32_t v, int32_t c) {
+    const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+    return max3((int32_t)r[0], (int32_t)r[1], c);
+}
 __device__ __forceinline__ int32_t half_sum(int32_t v) {
     const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
     return (int32_t)(r[0] + r[1]);
@@ -677,89 +683,6 @@ __device__ __forceinline__ int32_t exp2_fast(int32_t x, int32_t eM, int32_t rs) 
 // LDS wait covers both; the compiler's own packing of byte loads would take
 // 4.5 instructions per four bytes, and it would wait for the in-flight
 // stage copy before every LDS read.
-#define QF_LUT_LOADS                                   \
-    "ds_read_u8 %0, %0 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %1, %1 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %2, %2 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %3, %3 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %4, %4 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %5, %5 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %6, %6 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %7, %7 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %8, %8 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %9, %9 offset:%c[lut]\n\t"             \
-    "ds_read_u8 %10, %10 offset:%c[lut]\n\t"           \
-    "ds_read_u8 %11, %11 offset:%c[lut]\n\t"           \
-    "ds_read_u8 %12, %12 offset:%c[lut]\n\t"           \
-    "ds_read_u8 %13, %13 offset:%c[lut]\n\t"           \
-    "ds_read_u8 %14, %14 offset:%c[lut]\n\t"           \
-    "ds_read_u8 %15, %15 offset:%c[lut]\n\t"
-#define QF_LUT_PACK                                    \
-    "s_waitcnt lgkmcnt(0)\n\t"                          \
-    "v_lshl_or_b32 %0, %1, 8, %0\n\t"                   \
-    "v_lshl_or_b32 %2, %3, 8, %2\n\t"                   \
-    "v_lshl_or_b32 %0, %2, 16, %0\n\t"                  \
-    "v_lshl_or_b32 %4, %5, 8, %4\n\t"                   \
-    "v_lshl_or_b32 %6, %7, 8, %6\n\t"                   \
-    "v_lshl_or_b32 %4, %6, 16, %4\n\t"                  \
-    "v_lshl_or_b32 %8, %9, 8, %8\n\t"                   \
-    "v_lshl_or_b32 %10, %11, 8, %10\n\t"                \
-    "v_lshl_or_b32 %8, %10, 16, %8\n\t"                 \
-    "v_lshl_or_b32 %12, %13, 8, %12\n\t"                \
-    "v_lshl_or_b32 %14, %15, 8, %14\n\t"                \
-    "v_lshl_or_b32 %12, %14, 16, %12"
-#define QF_LUT_IDX_OPERANDS                                                                                  \
-    "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),         \
-        "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]), "+v"(r[12]), "+v"(r[13]), "+v"(r[14]), "+v"(r[15])
-
-template <int D, int LUT>
-__device__ __forceinline__ void lut_pack_vt(uint32_t* pk, i32x4* vf, const uint32_t* idx, const int8_t* lv,
-                                            const Frag<D>& fr) {
-    static_assert(LUT >= 0 && LUT + kLutMax <= 65536, "table offset must fit the 16-bit LDS immediate");
-    typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
-    const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)lv;
-    // each byte load writes its result over its own index register
-    uint32_t r[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) r[i] = idx[i];
-    i32x2 t[2 * (D / 32)];
-    if constexpr (D == 32) {
-        asm volatile(QF_LUT_LOADS
-                     "ds_read_b64_tr_b8 %[t0], %[b0]\n\t"
-                     "ds_read_b64_tr_b8 %[t1], %[b0] offset:%c[vo]\n\t" QF_LUT_PACK
-                     : QF_LUT_IDX_OPERANDS, [t0] "=&v"(t[0]), [t1] "=&v"(t[1])
-                     : [b0] "v"(base + fr.v[0]), [vo] "i"(16 * D), [lut] "i"(LUT));
-    } else if constexpr (D == 64) {
-        asm volatile(QF_LUT_LOADS
-                     "ds_read_b64_tr_b8 %[t0], %[b0]\n\t"
-                     "ds_read_b64_tr_b8 %[t1], %[b0] offset:%c[vo]\n\t"
-                     "ds_read_b64_tr_b8 %[t2], %[b1]\n\t"
-                     "ds_read_b64_tr_b8 %[t3], %[b1] offset:%c[vo]\n\t" QF_LUT_PACK
-                     : QF_LUT_IDX_OPERANDS, [t0] "=&v"(t[0]), [t1] "=&v"(t[1]), [t2] "=&v"(t[2]), [t3] "=&v"(t[3])
-                     : [b0] "v"(base + fr.v[0]), [b1] "v"(base + fr.v[1]), [vo] "i"(16 * D), [lut] "i"(LUT));
-    } else {
-        asm volatile(QF_LUT_LOADS
-                     "ds_read_b64_tr_b8 %[t0], %[b0]\n\t"
-                     "ds_read_b64_tr_b8 %[t1], %[b0] offset:%c[vo]\n\t"
-                     "ds_read_b64_tr_b8 %[t2], %[b1]\n\t"
-                     "ds_read_b64_tr_b8 %[t3], %[b1] offset:%c[vo]\n\t"
-                     "ds_read_b64_tr_b8 %[t4], %[b2]\n\t"
-                     "ds_read_b64_tr_b8 %[t5], %[b2] offset:%c[vo]\n\t"
-                     "ds_read_b64_tr_b8 %[t6], %[b3]\n\t"
-                     "ds_read_b64_tr_b8 %[t7], %[b3] offset:%c[vo]\n\t" QF_LUT_PACK
-                     : QF_LUT_IDX_OPERANDS, [t0] "=&v"(t[0]), [t1] "=&v"(t[1]), [t2] "=&v"(t[2]), [t3] "=&v"(t[3]),
-                       [t4] "=&v"(t[4]), [t5] "=&v"(t[5]), [t6] "=&v"(t[6]), [t7] "=&v"(t[7])
-                     : [b0] "v"(base + fr.v[0]), [b1] "v"(base + fr.v[1]), [b2] "v"(base + fr.v[2]),
-                       [b3] "v"(base + fr.v[3]), [vo] "i"(16 * D), [lut] "i"(LUT));
-    }
-#pragma unroll
-    for (int w = 0; w < 4; ++w) pk[w] = r[4 * w];
-#pragma unroll
-    for (int i = 0; i < D / 32; ++i) vf[i] = i32x4{t[2 * i].x, t[2 * i].y, t[2 * i + 1].x, t[2 * i + 1].y};
-}
-// The first TV score registers only (TV = 4, 8, 12: a partial last step of at
-// most 2*TV keys, whose registers TV..15 hold padded columns alone): pk[0 ..
-// TV/4 - 1] (the others 0) and the V^T fragments.
 #define QF_L(i) "ds_read_u8 %" #i ", %" #i " offset:%c[lut]\n\t"
 #define QF_P(a, b, c, d)                                      \
     "v_lshl_or_b32 %" #a ", %" #b ", 8, %" #a "\n\t"            \
@@ -768,43 +691,34 @@ __device__ __forceinline__ void lut_pack_vt(uint32_t* pk, i32x4* vf, const uint3
 #define QF_LOADS4 QF_L(0) QF_L(1) QF_L(2) QF_L(3)
 #define QF_LOADS8 QF_LOADS4 QF_L(4) QF_L(5) QF_L(6) QF_L(7)
 #define QF_LOADS12 QF_LOADS8 QF_L(8) QF_L(9) QF_L(10) QF_L(11)
+#define QF_LOADS16 QF_LOADS12 QF_L(12) QF_L(13) QF_L(14) QF_L(15)
 #define QF_PACK4 "s_waitcnt lgkmcnt(0)\n\t" QF_P(0, 1, 2, 3)
 #define QF_PACK8 QF_PACK4 QF_P(4, 5, 6, 7)
 #define QF_PACK12 QF_PACK8 QF_P(8, 9, 10, 11)
+#define QF_PACK16 QF_PACK12 QF_P(12, 13, 14, 15)
 #define QF_IDX4 "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3])
 #define QF_IDX8 QF_IDX4, "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7])
 #define QF_IDX12 QF_IDX8, "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11])
-#define QF_TR32                                           \
-    "ds_read_b64_tr_b8 %[t0], %[b0]\n\t"                  \
-    "ds_read_b64_tr_b8 %[t1], %[b0] offset:%c[vo]\n\t"
-#define QF_TR64 QF_TR32                                   \
-    "ds_read_b64_tr_b8 %[t2], %[b1]\n\t"                  \
-    "ds_read_b64_tr_b8 %[t3], %[b1] offset:%c[vo]\n\t"
-#define QF_TR128 QF_TR64                                  \
-    "ds_read_b64_tr_b8 %[t4], %[b2]\n\t"                  \
-    "ds_read_b64_tr_b8 %[t5], %[b2] offset:%c[vo]\n\t"    \
-    "ds_read_b64_tr_b8 %[t6], %[b3]\n\t"                  \
-    "ds_read_b64_tr_b8 %[t7], %[b3] offset:%c[vo]\n\t"
-#define QF_T32 [t0] "=&v"(t[0]), [t1] "=&v"(t[1])
-#define QF_T64 QF_T32, [t2] "=&v"(t[2]), [t3] "=&v"(t[3])
-#define QF_T128 QF_T64, [t4] "=&v"(t[4]), [t5] "=&v"(t[5]), [t6] "=&v"(t[6]), [t7] "=&v"(t[7])
-#define QF_B32 [b0] "v"(base + fr.v[0]), [vo] "i"(16 * D), [lut] "i"(LUT)
-#define QF_B64 QF_B32, [b1] "v"(base + fr.v[1])
-#define QF_B128 QF_B64, [b2] "v"(base + fr.v[2]), [b3] "v"(base + fr.v[3])
+#define QF_IDX16 QF_IDX12, "+v"(r[12]), "+v"(r[13]), "+v"(r[14]), "+v"(r[15])
 #define QF_TV_ASM(LOADS, PACK, IDX)                                                             \
     if constexpr (D == 32)                                                                      \
-        asm volatile(LOADS QF_TR32 PACK : IDX, QF_T32 : QF_B32);                                \
+        asm volatile(LOADS QF_TR32 PACK : IDX, QF_T32 : QF_B32, [lut] "i"(LUT));                \
     else if constexpr (D == 64)                                                                 \
-        asm volatile(LOADS QF_TR64 PACK : IDX, QF_T64 : QF_B64);                                \
+        asm volatile(LOADS QF_TR64 PACK : IDX, QF_T64 : QF_B64, [lut] "i"(LUT));                \
     else                                                                                        \
-        asm volatile(LOADS QF_TR128 PACK : IDX, QF_T128 : QF_B128);
-template <int D, int LUT, int TV>
-__device__ __forceinline__ void lut_pack_vtn(uint32_t* pk, i32x4* vf, const uint32_t* idx, const int8_t* lv,
-                                             const Frag<D>& fr) {
+        asm volatile(LOADS QF_TR128 PACK : IDX, QF_T128 : QF_B128, [lut] "i"(LUT));
+// The first TV score registers (TV = 16: all; TV = 4, 8, 12: a partial last
+// step of at most 2*TV keys, whose registers TV..15 hold padded columns
+// alone): pk[0 .. TV/4 - 1] (the others 0) and the V^T fragments of the tile
+// at LDS address vbase + VO (read_vt).
+template <int D, int LUT, int TV, int VO>
+__device__ __forceinline__ void lut_pack_vt(uint32_t* pk, i32x4* vf, const uint32_t* idx, uint32_t vbase,
+                                            const Frag<D>& fr) {
     static_assert(LUT >= 0 && LUT + kLutMax <= 65536, "table offset must fit the 16-bit LDS immediate");
-    static_assert(TV == 4 || TV == 8 || TV == 12, "4, 8 or 12 registers");
+    static_assert(VO >= 0 && VO + 16 * D < 65536, "offsets must fit the 16-bit LDS immediate");
+    static_assert(TV == 4 || TV == 8 || TV == 12 || TV == 16, "4, 8, 12 or 16 registers");
     typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
-    const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) int8_t*)lv;
+    // each byte load writes its result over its own index register
     uint32_t r[TV];
 #pragma unroll
     for (int i = 0; i < TV; ++i) r[i] = idx[i];
@@ -813,25 +727,83 @@ __device__ __forceinline__ void lut_pack_vtn(uint32_t* pk, i32x4* vf, const uint
         QF_TV_ASM(QF_LOADS4, QF_PACK4, QF_IDX4)
     } else if constexpr (TV == 8) {
         QF_TV_ASM(QF_LOADS8, QF_PACK8, QF_IDX8)
-    } else {
+    } else if constexpr (TV == 12) {
         QF_TV_ASM(QF_LOADS12, QF_PACK12, QF_IDX12)
+    } else {
+        QF_TV_ASM(QF_LOADS16, QF_PACK16, QF_IDX16)
     }
 #pragma unroll
     for (int w = 0; w < 4; ++w) pk[w] = 4 * w < TV ? r[4 * w < TV ? 4 * w : 0] : 0u;
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) vf[i] = i32x4{t[2 * i].x, t[2 * i].y, t[2 * i + 1].x, t[2 * i + 1].y};
 }
+// The full-step table path with the table check of a wave whose rows the host
+// bound does not cover (lut_mode 2): the loads go out first, and the check
+// (every column of the lane within lut_lim of the row maximum:
+// mn - min(s) <= lut_lim, unsigned) runs while they are in flight, instead of
+// deciding, before the loads, whether to issue them.  Returns the lanes that
+// pass; the caller falls back to the arithmetic unless all do.
+#define QF_S16                                                                                            \
+    [s0] "v"(s[0]), [s1] "v"(s[1]), [s2] "v"(s[2]), [s3] "v"(s[3]), [s4] "v"(s[4]), [s5] "v"(s[5]),          \
+        [s6] "v"(s[6]), [s7] "v"(s[7]), [s8] "v"(s[8]), [s9] "v"(s[9]), [s10] "v"(s[10]), [s11] "v"(s[11]),   \
+        [s12] "v"(s[12]), [s13] "v"(s[13]), [s14] "v"(s[14]), [s15] "v"(s[15]), [mn] "v"(mn), [lim] "s"(lim)
+#define QF_CHECK                                          \
+    "v_min3_i32 %[dm], %[s0], %[s1], %[s2]\n\t"           \
+    "v_min3_i32 %[dm], %[dm], %[s3], %[s4]\n\t"           \
+    "v_min3_i32 %[dm], %[dm], %[s5], %[s6]\n\t"           \
+    "v_min3_i32 %[dm], %[dm], %[s7], %[s8]\n\t"           \
+    "v_min3_i32 %[dm], %[dm], %[s9], %[s10]\n\t"          \
+    "v_min3_i32 %[dm], %[dm], %[s11], %[s12]\n\t"         \
+    "v_min3_i32 %[dm], %[dm], %[s13], %[s14]\n\t"         \
+    "v_min_i32 %[dm], %[dm], %[s15]\n\t"                  \
+    "v_sub_u32 %[dm], %[mn], %[dm]\n\t"                   \
+    "v_cmp_ge_u32_e64 %[ok], %[lim], %[dm]\n\t"
+template <int D, int LUT, int VO>
+__device__ __forceinline__ uint64_t lut_pack_vt_check(uint32_t* pk, i32x4* vf, const uint32_t* idx, uint32_t vbase,
+                                                      const Frag<D>& fr, const i32x16& s, int32_t mn, int32_t lim) {
+    static_assert(LUT >= 0 && LUT + kLutMax <= 65536, "table offset must fit the 16-bit LDS immediate");
+    static_assert(VO >= 0 && VO + 16 * D < 65536, "offsets must fit the 16-bit LDS immediate");
+    typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+    uint32_t r[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) r[i] = idx[i];
+    i32x2 t[2 * (D / 32)];
+    uint64_t ok;
+    int32_t dm;
+    if constexpr (D == 32)
+        asm volatile(QF_LOADS16 QF_TR32 QF_CHECK QF_PACK16
+                     : QF_IDX16, QF_T32, [ok] "=&s"(ok), [dm] "=&v"(dm)
+                     : QF_B32, [lut] "i"(LUT), QF_S16);
+    else if constexpr (D == 64)
+        asm volatile(QF_LOADS16 QF_TR64 QF_CHECK QF_PACK16
+                     : QF_IDX16, QF_T64, [ok] "=&s"(ok), [dm] "=&v"(dm)
+                     : QF_B64, [lut] "i"(LUT), QF_S16);
+    else
+        asm volatile(QF_LOADS16 QF_TR128 QF_CHECK QF_PACK16
+                     : QF_IDX16, QF_T128, [ok] "=&s"(ok), [dm] "=&v"(dm)
+                     : QF_B128, [lut] "i"(LUT), QF_S16);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) pk[w] = r[4 * w];
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) vf[i] = i32x4{t[2 * i].x, t[2 * i].y, t[2 * i + 1].x, t[2 * i + 1].y};
+    return ok;
+}
+#undef QF_S16
+#undef QF_CHECK
 #undef QF_L
 #undef QF_P
 #undef QF_LOADS4
 #undef QF_LOADS8
 #undef QF_LOADS12
+#undef QF_LOADS16
 #undef QF_PACK4
 #undef QF_PACK8
 #undef QF_PACK12
+#undef QF_PACK16
 #undef QF_IDX4
 #undef QF_IDX8
 #undef QF_IDX12
+#undef QF_IDX16
 #undef QF_TR32
 #undef QF_TR64
 #undef QF_TR128
@@ -842,9 +814,6 @@ __device__ __forceinline__ void lut_pack_vtn(uint32_t* pk, i32x4* vf, const uint
 #undef QF_B64
 #undef QF_B128
 #undef QF_TV_ASM
-#undef QF_LUT_LOADS
-#undef QF_LUT_PACK
-#undef QF_LUT_IDX_OPERANDS
 
 // Per-wave state of the fast kernel (S layout for m, l, bnd: lane = query;
 // O layout for acc).
@@ -913,7 +882,8 @@ __device__ __forceinline__ uint32_t umin_first(const i32x16& s) {
 }
 
 // S^T tile of one step with bias and padding applied (kernel.py:153-156, :250-253);
-// returns the row max over the 32 columns (both lane halves).
+// returns this lane's maximum over its 16 columns (the row's other 16 are in
+// lane ^ 32).
 // Every score carries kScoreBias, from an extra MFMA of xb (all bytes -128)
 // with itself (int32 arithmetic wraps, so differences are unchanged).
 // smin: the minimum over the real columns when MASKED or need_min (else
@@ -968,7 +938,7 @@ __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, uint32_t& sm
         for (int v = 0; v < 16; ++v)
             if (v >= TV || padded(v, tcut)) s[v] = PAD;
     }
-    return half_max(max_first<TV>(s));
+    return max_first<TV>(s);
 }
 
 // One 32-key step (qflash/kernel.py:147-174) for the 32 query rows of a wave.
@@ -979,25 +949,40 @@ __device__ __forceinline__ int32_t scores(i32x16& s, int32_t& smin, uint32_t& sm
 // the running maximum is the reference's one plus SB as long as no biased
 // value wraps (checked for masked steps; unmasked scores are bounded by
 // 128 * ||q||_1).  LUT: LDS address of the p table.
-template <int D, int LUT, bool MASKED, bool TAIL, bool WIDE, bool DYN, bool FIRST, int TV = 16>
+// TABM (unmasked waves): 0 = the path of each step is chosen from lut_mode;
+// 1 = the table path is proved for every step of the wave (lut_mode 1), so the
+// step has no other path; 2 = (lut_mode 2) full steps issue the table loads
+// first and check the table's range while they are in flight
+// (lut_pack_vt_check), falling back to the arithmetic when it fails.  The
+// step's K tile sits at lk, its V tile at LDS address vbase + VO (read_vt).
+template <int D, int LUT, bool MASKED, bool TAIL, bool WIDE, bool DYN, bool FIRST, int TABM, int VO, int TV = 16>
 __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const i32x4* qv, const int8_t* lk,
-                                          const int8_t* lv, const Frag<D>& fr, const BiasRow& brow, int kstart,
+                                          uint32_t vbase, const Frag<D>& fr, const BiasRow& brow, int kstart,
                                           int lane, bool wave_fast, int32_t xlim, int lut_mode, i32x4 xb) {
     constexpr int DB = D / 32;
     constexpr int32_t SB = kScoreBias;
     const int g = lane >> 5;
     const int32_t rs = a.rs, eM = a.eM, rM = a.rM;
+    // lut_n - 1 as an opaque scalar: the compiler would otherwise form the
+    // threshold m' - (lut_n - 1) with two vector operations
+    int32_t lut_n1 = a.lut_n - 1;
+    asm volatile("" : "+s"(lut_n1));
 
+    // speculative table path of this step (TABM 2)
+    constexpr bool SPEC = TABM == 2 && !MASKED && !TAIL;
     int32_t bias_v[16];
     if constexpr (MASKED) load_bias<TAIL>(bias_v, a, brow, kstart, lane);
     i32x16 s;
     int32_t smin;
     uint32_t sminu;
     static_assert(TV == 16 || (TAIL && (TV == 4 || TV == 8 || TV == 12)), "TV < 16: partial steps of <= 2*TV keys");
-    const int32_t mx =
-        scores<D, MASKED, TAIL, TV>(s, smin, sminu, a, qv, lk, fr, bias_v, kstart, lane, lut_mode == 2, xb);
+    const int32_t mxl =
+        scores<D, MASKED, TAIL, TV>(s, smin, sminu, a, qv, lk, fr, bias_v, kstart, lane, SPEC ? false : lut_mode == 2,
+                                    xb);
     const int32_t m = st.m;
-    int32_t mn = max(m, mx);  // kernel.py:158
+    // opaque: the compiler would otherwise test "row changed" on an
+    // intermediate maximum and split the three-input max in two
+    int32_t mn = opaque(half_max3(mxl, m));  // kernel.py:158
     constexpr bool first = FIRST;  // kstart == 0
 
     // Table path.  Unmasked: every real column of the wave has u = m' - s <=
@@ -1016,13 +1001,23 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     // combined without short-circuit branches.
     bool lut_ok;
     int32_t slo = smin;
+    uint32_t pk[4];
+    i32x4 vf[DB];
     if constexpr (MASKED) {
         slo = min(smin, m);
         const bool far_ok = (mn >= a.far_lo) & ((uint32_t)(mn - slo) <= (uint32_t)a.far_hi);
         const bool near_ok = (uint32_t)mn - min(sminu, (uint32_t)mn) <= (uint32_t)a.lut_lim;
         lut_ok = lut_mode == 2 && __all(far_ok & near_ok);
+    } else if constexpr (SPEC) {
+        // the table path's indices (as below); pk and vf are its result when every lane passes
+        const int32_t thr = wsub(mn, lut_n1);
+        uint32_t idx[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) idx[v] = __builtin_elementwise_sub_sat((uint32_t)s[v], (uint32_t)thr);
+        const uint64_t okm = lut_pack_vt_check<D, LUT, VO>(pk, vf, idx, vbase, fr, s, mn, a.lut_lim);
+        lut_ok = okm == __builtin_amdgcn_read_exec();
     } else {
-        lut_ok = lut_mode == 1 || (lut_mode == 2 && __all((uint32_t)(mn - smin) <= (uint32_t)a.lut_lim));
+        lut_ok = TABM == 1 || lut_mode == 1 || (lut_mode == 2 && __all((uint32_t)(mn - smin) <= (uint32_t)a.lut_lim));
     }
     // 24-bit arithmetic path: masked steps check |x| <= xlim and the 24-bit
     // operand range (then mn - slo < 2^24 is exact in int32), evaluated only
@@ -1033,14 +1028,13 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
         else
             return wave_fast;
     };
-    uint32_t pk[4];
-    i32x4 vf[DB];
-    if (lut_ok) {
+    if (__builtin_expect(lut_ok, SPEC)) {
+        if constexpr (!SPEC) {
         // table index max(s - thr, 0) = lut_n - 1 - min(u, lut_n - 1) with one
         // unsigned saturating subtraction: thr in [0, 2^31) and, for the
         // columns it serves, s in [0, 2^31) (unmasked: s >= SB - 128 * ||q||_1
         // > lut_n - 1, lut_mode != 0 only then)
-        const int32_t thr = wsub(mn, a.lut_n - 1);
+        const int32_t thr = wsub(mn, lut_n1);
         uint32_t idx[16];
         if constexpr (MASKED) {
             // s' < 0 reads as >= 2^31 > thr + lut_n - 1: clamped to entry lut_n = far_p
@@ -1057,10 +1051,8 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
             for (int v = 0; v < TV; ++v)
                 if (padded(v, tcut)) idx[v] = 0;
         }
-        if constexpr (TV < 16)
-            lut_pack_vtn<D, LUT, TV>(pk, vf, idx, lv, fr);
-        else
-            lut_pack_vt<D, LUT>(pk, vf, idx, lv, fr);
+        lut_pack_vt<D, LUT, TV, VO>(pk, vf, idx, vbase, fr);
+        }
     } else if (vec_ok()) {
         // kernel.py:159-161 in six ops per score (see the fast-path comment)
         const int32_t c1 = opaque(wadd(wmul(wsub(0, mn), eM), 1 << 16));
@@ -1114,7 +1106,11 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
         }
     }
     // kernel.py:162
-    int32_t lij = __builtin_amdgcn_sdot4((int)pk[0], 0x01010101, 0, false);
+    // the first dot product takes the constant from a scalar register, so that
+    // its accumulator can be the inline 0 (no register cleared beforehand)
+    int32_t ones, lij;
+    asm("s_mov_b32 %0, 0x1010101" : "=s"(ones));
+    asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(lij) : "v"(pk[0]), "s"(ones));
     lij = __builtin_amdgcn_sdot4((int)pk[1], 0x01010101, lij, false);
     lij = __builtin_amdgcn_sdot4((int)pk[2], 0x01010101, lij, false);
     lij = __builtin_amdgcn_sdot4((int)pk[3], 0x01010101, lij, false);
@@ -1193,12 +1189,12 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
             auto pair = [&]<int V>() {
                 constexpr int rlo = 8 * (V >> 2) + (V & 3);
                 if (__builtin_expect((pairs >> rlo) & 1u, 0)) {
-                    const int32_t av = __builtin_amdgcn_update_dpp(0, rlo < 16 ? m1 : m2, 0x150 + (rlo & 15), 0xf,
-                                                                   0xf, false);
+                    // every lane reads a valid source lane: no old value needed
+                    const int32_t av = __builtin_amdgcn_mov_dpp(rlo < 16 ? m1 : m2, 0x150 + (rlo & 15), 0xf, 0xf,
+                                                                false);
                     int32_t ah = 0;
                     if constexpr (WIDE)
-                        ah = wide ? __builtin_amdgcn_update_dpp(0, rlo < 16 ? h1 : h2, 0x150 + (rlo & 15), 0xf, 0xf,
-                                                                false)
+                        ah = wide ? __builtin_amdgcn_mov_dpp(rlo < 16 ? h1 : h2, 0x150 + (rlo & 15), 0xf, 0xf, false)
                                   : 0;
 #pragma unroll
                     for (int t = 0; t < DB; ++t) {
@@ -1224,7 +1220,7 @@ __device__ __forceinline__ void fast_step(FastState<D>& st, const Args& a, const
     }
     // O += P . V (kernel.py:171)
     const i32x4 pa = i32x4{(int32_t)pk[0], (int32_t)pk[1], (int32_t)pk[2], (int32_t)pk[3]};
-    if (!lut_ok) read_vt<D>(vf, lv, fr);
+    if (!SPEC && !lut_ok) read_vt<D, VO>(vf, vbase, fr);  // (SPEC: read with the table)
 #pragma unroll
     for (int t = 0; t < DB; ++t) st.acc[t] = mfma32(pa, vf[t], st.acc[t]);
     st.m = mn;  // kernel.py:172
@@ -1297,7 +1293,7 @@ __device__ __forceinline__ void fast_store(const FastState<D>& st, const Args& a
 // buffer, which no later copy overwrites, then the rows' int8 codes.  Every
 // wave of the workgroup issues its share of the copies and passes the same
 // barriers, active or not.
-template <int D, int W, bool MASKED, bool WIDE, bool DYN>
+template <int D, int W, bool MASKED, bool WIDE, bool DYN, int TABM>
 __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t* smem, const int8_t* kb,
                                           const int8_t* vb, int z, int h, const BiasRow& brow, int wave, int lane,
                                           int q0, bool active, bool wave_fast, int32_t xlim, int lut_mode) {
@@ -1322,6 +1318,7 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
         __builtin_amdgcn_make_buffer_rsrc((void*)vb, 0, (a.N - 1) * (int32_t)a.sv[2] + D, 0x00020000);
     const StageDma<D, W> dma(a, wave, lane);
     const Frag<D> fr(lane);
+    const uint32_t lds0 = lds_addr(smem);  // a constant: the kernel's LDS array
     dma.issue(rk, rv, smem, 0, a, wave);
     stage_sync();
 
@@ -1331,46 +1328,72 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
     // step 0 (m = NEG_INF, acc = 0) apart from the loop: the loop body then
     // carries no first-step cases
     if (active && nfull > 0)
-        fast_step<D, LUT, MASKED, false, WIDE, DYN, true>(st, a, qv, smem, smem + S::KBYTES, fr, brow, 0, lane,
-                                                          wave_fast, xlim, lut_mode, xb);
-    for (int stg = 0; stg < nstage; ++stg) {
-        const int8_t* buf = smem + (stg & 1) * S::BYTES;
-        if (stg + 1 < nstage) dma.issue(rk, rv, smem + ((stg + 1) & 1) * S::BYTES, (stg + 1) * S::KEYS, a, wave);
+        fast_step<D, LUT, MASKED, false, WIDE, DYN, true, TABM, S::KBYTES>(st, a, qv, smem, lds0, fr, brow, 0, lane,
+                                                                        wave_fast, xlim, lut_mode, xb);
+    // One stage in LDS buffer B (compile-time, like the steps within it, so that
+    // every K and V^T fragment read takes its tile offset as an immediate).
+    auto stage = [&]<int B>(int stg) {
+        if (stg + 1 < nstage) dma.issue(rk, rv, smem + (1 - B) * S::BYTES, (stg + 1) * S::KEYS, a, wave);
         if (active) {
-            // unrolled: the steps' LDS offsets within the stage are immediates
-#pragma unroll
-            for (int half = 0; half < S::STEPS; ++half) {
-                const int step = stg * S::STEPS + half;
-                if (half == 0 && stg == 0) continue;  // step 0 ran above
-                if (step >= nfull) break;
+            auto one = [&]<int HS>() {
+                const int step = stg * S::STEPS + HS;
+                if ((B == 0 && HS == 0 && stg == 0) || step >= nfull) return;  // step 0 ran above
                 if constexpr (!MASKED) asm volatile("" : "+v"(xb));  // masked: C = bias, not hoistable
-                fast_step<D, LUT, MASKED, false, WIDE, DYN, false>(st, a, qv, buf + half * 32 * D,
-                                                                   buf + S::KBYTES + half * 32 * D, fr, brow,
-                                                                   step * 32, lane, wave_fast, xlim, lut_mode, xb);
-            }
+                constexpr int KO = B * S::BYTES + HS * 32 * D;
+                fast_step<D, LUT, MASKED, false, WIDE, DYN, false, TABM, KO + S::KBYTES>(
+                    st, a, qv, smem + KO, lds0, fr, brow, step * 32, lane, wave_fast, xlim, lut_mode, xb);
+            };
+            [&]<int... HS>(std::integer_sequence<int, HS...>) { (one.template operator()<HS>(), ...); }(
+                std::make_integer_sequence<int, S::STEPS>{});
         }
         stage_sync();
+    };
+    if constexpr (TABM != 0) {
+        for (int stg = 0; stg < nstage; stg += 2) {
+            stage.template operator()<0>(stg);
+            if (stg + 1 < nstage) stage.template operator()<1>(stg + 1);
+        }
+    } else {
+        // the loops with more than the table path: one stage body with the
+        // buffer's address in a register (their registers do not fit otherwise)
+        for (int stg = 0; stg < nstage; ++stg) {
+            const int8_t* buf = smem + (stg & 1) * S::BYTES;
+            if (stg + 1 < nstage) dma.issue(rk, rv, smem + ((stg + 1) & 1) * S::BYTES, (stg + 1) * S::KEYS, a, wave);
+            if (active) {
+#pragma unroll
+                for (int half = 0; half < S::STEPS; ++half) {
+                    const int step = stg * S::STEPS + half;
+                    if (half == 0 && stg == 0) continue;  // step 0 ran above
+                    if (step >= nfull) break;
+                    if constexpr (!MASKED) asm volatile("" : "+v"(xb));  // masked: C = bias, not hoistable
+                    fast_step<D, LUT, MASKED, false, WIDE, DYN, false, TABM, 0>(
+                        st, a, qv, buf + half * 32 * D, lds_addr(buf + S::KBYTES + half * 32 * D), fr, brow,
+                        step * 32, lane, wave_fast, xlim, lut_mode, xb);
+                }
+            }
+            stage_sync();
+        }
     }
     if (active && (a.N & 31)) {
         const int8_t* buf = smem + ((nstage - 1) & 1) * S::BYTES;
         const int th = nfull % S::STEPS;
         const int8_t* lk = buf + th * 32 * D;
-        const int8_t* lv = buf + S::KBYTES + th * 32 * D;
+        const uint32_t lv = lds_addr(buf + S::KBYTES + th * 32 * D);
         if (nfull == 0)
-            fast_step<D, LUT, MASKED, true, WIDE, DYN, true>(st, a, qv, lk, lv, fr, brow, 0, lane, wave_fast, xlim,
-                                                             lut_mode, xb);
+            fast_step<D, LUT, MASKED, true, WIDE, DYN, true, TABM, 0>(st, a, qv, lk, lv, fr, brow, 0, lane, wave_fast,
+                                                                    xlim, lut_mode, xb);
         else if ((a.N & 31) <= 8)  // keys of the first TV score registers only
-            fast_step<D, LUT, MASKED, true, WIDE, DYN, false, 4>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane,
-                                                                 wave_fast, xlim, lut_mode, xb);
+            fast_step<D, LUT, MASKED, true, WIDE, DYN, false, TABM, 0, 4>(st, a, qv, lk, lv, fr, brow, nfull * 32,
+                                                                        lane, wave_fast, xlim, lut_mode, xb);
         else if ((a.N & 31) <= 16)
-            fast_step<D, LUT, MASKED, true, WIDE, DYN, false, 8>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane,
-                                                                 wave_fast, xlim, lut_mode, xb);
+            fast_step<D, LUT, MASKED, true, WIDE, DYN, false, TABM, 0, 8>(st, a, qv, lk, lv, fr, brow, nfull * 32,
+                                                                        lane, wave_fast, xlim, lut_mode, xb);
         else if ((a.N & 31) <= 24)
-            fast_step<D, LUT, MASKED, true, WIDE, DYN, false, 12>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane,
-                                                                  wave_fast, xlim, lut_mode, xb);
+            fast_step<D, LUT, MASKED, true, WIDE, DYN, false, TABM, 0, 12>(st, a, qv, lk, lv, fr, brow, nfull * 32,
+                                                                         lane, wave_fast, xlim, lut_mode, xb);
         else
-            fast_step<D, LUT, MASKED, true, WIDE, DYN, false>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane,
-                                                              wave_fast, xlim, lut_mode, xb);
+            fast_step<D, LUT, MASKED, true, WIDE, DYN, false, TABM, 0>(st, a, qv, lk, lv, fr, brow, nfull * 32, lane,
+                                                                     wave_fast, xlim, lut_mode, xb);
     }
     if (!active) return;
     // this wave's 256 bytes of the stage buffer that no step reads any more:
@@ -1384,8 +1407,11 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
 // O accumulators (D/32 x 16 VGPRs) and the score / exp temporaries.  D = 32
 // fits 6 (80 VGPRs, no spills; measured 5 % faster than 4 on Swin windows,
 // 8 slower).
+#ifndef QF_FAST_WAVES_D32
+#define QF_FAST_WAVES_D32 6
+#endif
 template <int D>
-constexpr int fast_waves_per_simd() { return D <= 32 ? 6 : (D == 64 ? QF_FAST_WAVES_D64 : 2); }
+constexpr int fast_waves_per_simd() { return D <= 32 ? QF_FAST_WAVES_D32 : (D == 64 ? QF_FAST_WAVES_D64 : 2); }
 
 // One workgroup of the single-tile kernel: row block mb (32 * W rows) of head
 // zh, in the LDS array smem whose table the caller has filled (visible after
@@ -1455,19 +1481,26 @@ __device__ __forceinline__ void fast_block(const Args& a, int8_t* smem, int zh, 
     }
 
     // Unmasked waves whose guard holds run a loop that never meets an alpha
-    // outside [-1, rs] after the first step; the others (and masked waves) run
-    // the loop that also handles it.  Both pass the same barriers, and each
-    // writes its own rows, so the two never merge register state.
+    // outside [-1, rs] after the first step (and, when the table serves every
+    // step, a loop with the table path alone); the others (and masked waves)
+    // run the loop that also handles it.  All pass the same barriers, and each
+    // writes its own rows, so they never merge register state.
     if constexpr (!MASKED) {
-        if (wave_fast)
-            fast_rows<D, W, false, false, DYN>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active, wave_fast, xlim,
-                                               lut_mode);
+        if (wave_fast && lut_mode == 1)
+            fast_rows<D, W, false, false, DYN, 1>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active,
+                                                  wave_fast, xlim, lut_mode);
+        else if (wave_fast && lut_mode == 2)
+            fast_rows<D, W, false, false, DYN, 2>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active,
+                                                  wave_fast, xlim, lut_mode);
+        else if (wave_fast)
+            fast_rows<D, W, false, false, DYN, 0>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active,
+                                                  wave_fast, xlim, lut_mode);
         else
-            fast_rows<D, W, false, true, DYN>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active, wave_fast, xlim,
-                                               lut_mode);
+            fast_rows<D, W, false, true, DYN, 0>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active,
+                                                 wave_fast, xlim, lut_mode);
     } else {
-        fast_rows<D, W, true, true, DYN>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active, wave_fast, xlim,
-                                               lut_mode);
+        fast_rows<D, W, true, true, DYN, 0>(a, qv, smem, kb, vb, z, h, brow, wave, lane, q0, active, wave_fast,
+                                            xlim, lut_mode);
     }
 }
 
