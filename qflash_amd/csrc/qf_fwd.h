@@ -847,9 +847,13 @@ __device__ __forceinline__ void load_bias(int32_t* bias_v, const Args& a, const 
             for (int e = 0; e < 4; ++e) bias_v[4 * k4 + e] = b[e];
         }
     } else {
+        // (rare layouts) the key of register v is k0 + 8*(v/4) + v%4: offsets from one
+        // opaque base, so that the compiler keeps no per-register constants live
+        // across the kernel for this path
+        const int k0 = opaque(kstart + 4 * (lane >> 5));
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-            const int key = kstart + crow(v, lane);
+            const int key = k0 + 8 * (v >> 2) + (v & 3);
             bias_v[v] = ((!TAIL || key < a.N) && br.row) ? br.row[(int64_t)key * a.sb[3]] : 0;
         }
     }
@@ -1405,10 +1409,10 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
 
 // Occupancy target (waves per SIMD) by head dim: the register budget of the
 // O accumulators (D/32 x 16 VGPRs) and the score / exp temporaries.  D = 32
-// fits 6 (80 VGPRs, no spills; measured 5 % faster than 4 on Swin windows,
-// 8 slower).
+// runs at 5 (the masked kernel needs 83 VGPRs; at 6, 80 VGPRs, it spills to
+// scratch, and measured on Swin windows it is 1.5 % slower).
 #ifndef QF_FAST_WAVES_D32
-#define QF_FAST_WAVES_D32 6
+#define QF_FAST_WAVES_D32 5
 #endif
 template <int D>
 constexpr int fast_waves_per_simd() { return D <= 32 ? QF_FAST_WAVES_D32 : (D == 64 ? QF_FAST_WAVES_D64 : 2); }
