@@ -268,6 +268,45 @@ def test_table_path_at_score_bias_edge(sm_scale, hip_hooks):
     assert int((o.cpu().numpy() != want).sum()) == 0
 
 
+@pytest.mark.parametrize("seed", [0, 1])
+def test_speculative_table_check_fails_mid_row(seed):
+    """cfg3's constants (kappa < 0: the table's zero range ends at u = 17455)
+    on rows whose host bound (2 * 128 * ||q||_1 ~ 74k) does not cover it, so
+    every wave runs the loop that issues each step's table loads before the
+    range check.  One key far below the scores (step 3) and one far above
+    them (step 12) put columns beyond the range: the check fails in those
+    steps and every later one, and the step falls back to the arithmetic;
+    the steps in between pass.  Codes equal the oracle's."""
+    import ctypes
+    from qflash_amd.kernel import fixed_point_constants
+    consts = Consts(*fixed_point_constants(0.017487, 30, 30))
+    assert (consts.sm_rscale, consts.exp_M) == (57, -1146)
+    n, lim = ctypes.c_int32(), ctypes.c_int32()
+    _lib().load().qflash_hip_lut_bounds(consts.sm_rscale, consts.exp_M, consts.req_M, ctypes.byref(n),
+                                        ctypes.byref(lim))
+    g = np.random.default_rng(seed)
+    Z, H, N, D = 1, 4, 577, 64
+    q = g.integers(-8, 9, (Z, H, N, D))
+    k = g.integers(-8, 9, (Z, H, N, D))
+    v = g.integers(-128, 128, (Z, H, N, D))
+    # the key at 100 opposes every query (its scores ~ -128 ||q||_1), the one at
+    # 400 follows it (+127 ||q||_1); both lie far outside lut_lim of the others
+    sgn = np.sign(q.sum(axis=2, keepdims=True))
+    sgn[sgn == 0] = 1
+    k[:, :, 100, :] = np.where(sgn[:, :, 0, :] > 0, -128, 127)
+    k[:, :, 400, :] = np.where(sgn[:, :, 0, :] > 0, 127, -128)
+    X = 2 * 128 * np.abs(q).sum(-1)
+    print(f"[case] seed={seed} consts={consts} lut=({n.value}, {lim.value}) X in [{X.min()}, {X.max()}]", flush=True)
+    assert X.min() > lim.value and X.max() // 2 + 4096 <= 1 << 19  # lut_mode 2 for every wave
+    q8, k8, v8 = (torch.from_numpy(x.astype(np.int8)) for x in (q, k, v))
+    want = oracle_c.attention_codes(q8, k8, v8, consts, Flags(), threads=8)
+    qd, kd, vd = q8.to(DEV), k8.to(DEV), v8.to(DEV)
+    o = torch.empty_like(vd)
+    _launch(qd, kd, vd, o, consts, Flags())
+    torch.cuda.synchronize()
+    assert int((o.cpu().numpy() != want).sum()) == 0
+
+
 TAIL_MODES = {  # hooks, score spread
     "table": (("FORCE_LUT",), 4.0),     # every step on the table
     "mixed": (("FORCE_LUT",), 40.0),    # wide spreads: some steps fail the per-step table check
