@@ -16,6 +16,8 @@ resident in HBM.  Prints ONE JSON line:
              x seeds 0, 1, 2: us/call, flushed us/call, TOPS, fractions of
              the MFMA peak and of the roofline, SQNR, end-to-end us (eager
              qflash.forward, and one replay of it captured in a HIP graph)
+  qkv_int8   the int8 QKV projection fused with the quantiser (not in the
+             reference) against the fp32 Linear + quantiser at cfg3's shape
 
 Timing: `--settle-ms` of back-to-back launches first (the clocks reach their
 loaded state), then W warmup launches, then K timed ones.
@@ -281,6 +283,52 @@ def per_config(dev, head=None, seeds=(0, 1, 2)):
     return out
 
 
+def qkv_int8_block(dev, reps: int = 20) -> dict:
+    """The int8 QKV projection fused with the quantiser (not in the reference;
+    QAttention.set_int8_proj) at cfg3's projection shape (B=64, N=577, C=768,
+    H=12), beside what it replaces: the fp32 qkv Linear plus quantize_qkv of
+    its q, k, v views (the module path before the attention).  Median of HIP
+    event times per call; int8 TOPS count one projection, 2*M*3C*C ops."""
+    import torch
+
+    from qflash_amd.kernel import int8_weights, qkv_int8, quantize_qkv
+
+    B, N, C, H = 64, 577, 768, 12
+    g = torch.Generator(device="cpu").manual_seed(0)
+    x = torch.randn(B, N, C, generator=g).to(dev)
+    lin = torch.nn.Linear(C, 3 * C).to(dev)
+    w8, w_scale = int8_weights(lin.weight)
+    bias = lin.bias.detach()
+
+    def fp32_path():
+        qkv = lin(x).reshape(B, N, 3, H, C // H).permute(2, 0, 3, 1, 4)
+        sc, fin = quantize_qkv(qkv[0], qkv[1], qkv[2])
+        return fin()
+
+    def int8_path():
+        return qkv_int8(x, w8, w_scale, bias, H)
+
+    def median_us(f):
+        with torch.no_grad():
+            for _ in range(5):
+                f()
+            torch.cuda.synchronize()
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+            for a, b in ev:
+                a.record()
+                f()
+                b.record()
+            torch.cuda.synchronize()
+        return statistics.median(a.elapsed_time(b) for a, b in ev) * 1e3
+
+    ops = 2 * B * N * 3 * C * C
+    fp32_us, int8_us = median_us(fp32_path), median_us(int8_path)
+    return {"shape": {"B": B, "N": N, "C": C, "H": H}, "fp32_linear_plus_quantize_us": fp32_us,
+            "int8_fused_us": int8_us, "speedup": fp32_us / int8_us, "projection_ops": ops,
+            "int8_tops_whole_op": ops / (int8_us * 1e-6) / 1e12,
+            "note": "int8 path: activation absmax + codes, two int8 MFMA GEMM passes (absmax, then codes), scales"}
+
+
 def e2e_call(w, dev):
     """The whole op on fp inputs already on the device: qflash.forward (scales,
     the host sync, constants, quantisation, bias, kernel, dequantisation), or
@@ -375,6 +423,8 @@ def main(argv=None):
                     help="with --profile: cfg3-distributed inputs of this shape instead of --config")
     ap.add_argument("--profile-e2e", action="store_true",
                     help="only the end-to-end op (warmup + steps calls, synchronised each) for rocprofv3 runs")
+    ap.add_argument("--profile-proj", action="store_true",
+                    help="only the int8 QKV projection (qkv_int8 at cfg3's shape), warmup + steps calls")
     ap.add_argument("--dense-bias", action="store_true",
                     help="with --profile-e2e on a Swin config: the materialised (B_, H, N, N) mask path")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
@@ -400,6 +450,10 @@ def main(argv=None):
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes": n, "copies": 10}), flush=True)
+        return 0
+    if args.profile_proj:
+        r = qkv_int8_block(dev, reps=max(1, args.steps))
+        print(json.dumps(r), flush=True)
         return 0
     if args.profile_e2e:
         w = prepare(args.config, args.seed, dev, dense_bias=args.dense_bias)
@@ -470,6 +524,7 @@ def main(argv=None):
     line["config"].update(Z=c.Z, H=c.H, N=c.N, D=c.D)
     if not args.no_per_config:
         line["per_config"] = per_config(dev, head)
+        line["qkv_int8"] = qkv_int8_block(dev)
     print(json.dumps(line), flush=True)
     return 0
 

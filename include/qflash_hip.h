@@ -111,6 +111,33 @@ int qflash_hip_scales(const void* q, const void* k, const void* v, int32_t dtype
                       void* scales, uint32_t* workspace, int64_t workspace_elems, void* stream);
 
 /*
+ * int8 QKV projection fused with the quantiser: the codes and scales of the
+ * q, k, v inputs of the attention straight from the activations, with the
+ * projection itself on int8 MFMA.  No counterpart in the reference, which
+ * computes the projection in floating point (qflash/attention.py:23-24) and
+ * quantises its output (qflash/kernel.py:294-311); this is its int8 variant,
+ * for callers that accept an int8 projection (QAttention(int8_proj=True)).
+ *   acc[m, c] = sum_k x8[m, k] * w8[c, k]                    (exact int32)
+ *   y[m, c]   = RN_fp32(RN_fp32(fp32(acc) * RN_fp32(x_scale * w_scale[c])) + bias[c])
+ *               (no bias term when bias is NULL)
+ * y's column thirds [0, C), [C, 2C), [2C, 3C) (C = Nc / 3) are q, k, v; scales
+ * and codes are what qflash_hip_scales and qflash_hip_quantize (fp32) would
+ * write for them: scales[0..2] = amax|q|, amax|k|, amax|v| times RN(1/127),
+ * scales[3] = scales[0] * scales[1]; codes[m, c] = clamp(rint(y / scale)).
+ * y itself is never stored: one pass reduces its absmax, a second recomputes it
+ * and writes the codes.
+ * x8: M x K int8 row-major (the activations' codes, x_scale their device fp32
+ * scale); w8: Nc x K int8 row-major, w_scale / bias: Nc fp32 (device);
+ * scales: 4 fp32 (device); codes: M x Nc int8 row-major (token-major q, k, v:
+ * codes + 0, + C, + 2C with row stride Nc).  K a multiple of 32, Nc = 3 C
+ * with C a multiple of 32.  workspace: as for qflash_hip_scales (zero before
+ * the first call, zero again after each).  Allocates nothing.
+ */
+int qflash_hip_qkv_int8(const int8_t* x8, const int8_t* w8, const float* w_scale, const float* bias,
+                        const float* x_scale, int32_t M, int32_t K, int32_t Nc, float* scales, int8_t* codes,
+                        uint32_t* workspace, int64_t workspace_elems, void* stream);
+
+/*
  * qflash_hip_scales without a workspace argument and without any allocation,
  * for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  No

@@ -35,6 +35,11 @@ Pinning status per function (what fails if the restatement is wrong):
 * sqnr_db: hand-computed norms; softmax_attention_fp32: closed forms (equal
   logits -> mean of V, a dominant logit -> its V row, -inf bias); both with
   planted mistakes (tests/test_oracle_host.py).
+* qkv_int8_ref (the int8 QKV projection, which has no counterpart in the
+  reference): its int32 products against pure-Python loops, its fp32 values
+  against float64 within their rounding, its codes against quantize_ref_torch
+  and its scales against amax / 127, with planted mistakes
+  (tests/test_oracle_proj.py).
 """
 from __future__ import annotations
 
@@ -383,3 +388,38 @@ def softmax_attention_fp32(q, k, v, bias=None, scale: float | None = None):
     if bias is not None:
         s = s + torch.as_tensor(bias, dtype=torch.float32)
     return torch.matmul(torch.softmax(s, dim=-1), v)
+
+
+def qkv_int8_ref(x8, w8, x_scale, w_scale, bias=None):
+    """The int8 QKV projection fused with the quantiser (qflash_hip_qkv_int8;
+    no counterpart in the reference, which projects in floating point,
+    qflash/attention.py:23-24, and quantises the result, kernel.py:294-311).
+
+    x8: (M, K) int8, w8: (Nc, K) int8, x_scale: fp32 scalar, w_scale and bias:
+    (Nc,) fp32.  acc = x8 . w8^T exactly; y = RN(RN(fp32(acc) * RN(x_scale *
+    w_scale)) + bias) in fp32; for the column thirds q, k, v (C = Nc / 3):
+    scale_t = RN(amax|y_t| * RN(1/127)) and codes clamp(rint(RN(y_t /
+    scale_t)), -128, 127) (0 where the quotient is NaN).  Returns the (M, Nc)
+    int8 codes and the 4 fp32 scales (q, k, v, q * k)."""
+    x8 = np.asarray(x8, dtype=np.int64)
+    w8 = np.asarray(w8, dtype=np.int64)
+    acc = x8 @ w8.T
+    assert np.abs(acc).max(initial=0) < (1 << 24), "fp32(acc) must be exact"
+    g = np.float32(x_scale) * np.asarray(w_scale, dtype=np.float32)
+    y = acc.astype(np.float32) * g[None, :]
+    if bias is not None:
+        y = y + np.asarray(bias, dtype=np.float32)[None, :]
+    C = y.shape[1] // 3
+    inv127 = np.float32(1.0 / 127.0)
+    scales = np.zeros(4, dtype=np.float32)
+    codes = np.zeros(y.shape, dtype=np.int8)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        for t in range(3):
+            yt = y[:, t * C:(t + 1) * C]
+            st = np.float32(np.abs(yt).max()) * inv127
+            scales[t] = st
+            qt = np.rint(yt / st)
+            qt = np.where(np.isnan(qt), 0, np.clip(qt, -128, 127))
+            codes[:, t * C:(t + 1) * C] = qt.astype(np.int8)
+    scales[3] = scales[0] * scales[1]
+    return codes, scales

@@ -31,7 +31,7 @@ class Flags(ctypes.Structure):
 
 
 EXPORTS = ("qflash_hip_kernel", "qflash_hip_masked_kernel", "qflash_hip_window_kernel", "qflash_hip_forward",
-           "qflash_hip_scales", "qflash_hip_scales_noalloc",
+           "qflash_hip_scales", "qflash_hip_scales_noalloc", "qflash_hip_qkv_int8",
            "qflash_hip_quantize", "qflash_hip_window_bias", "qflash_hip_mask_bias", "qflash_hip_constants",
            "qflash_hip_forward_planned", "qflash_hip_window_bias_planned", "qflash_hip_mask_bias_planned",
            "qflash_hip_last_error",
@@ -67,6 +67,8 @@ def _declare(L):
                                            fp, vp]
     L.qflash_hip_scales.restype = ctypes.c_int
     L.qflash_hip_scales.argtypes = [vp, vp, vp, i32, i64p, vp, vp, ctypes.c_int64, vp]
+    L.qflash_hip_qkv_int8.restype = ctypes.c_int
+    L.qflash_hip_qkv_int8.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp, ctypes.c_int64, vp]
     L.qflash_hip_scales_noalloc.restype = ctypes.c_int
     L.qflash_hip_scales_noalloc.argtypes = [vp, vp, vp, i32, i64p, vp, vp]
     L.qflash_hip_quantize.restype = ctypes.c_int

@@ -19,7 +19,7 @@ from typing import Dict, Iterable, Optional
 import torch
 from torch import nn
 
-from .kernel import qflash, qflash_forward_window
+from .kernel import LOG2E, forward_codes, int8_weights, qflash, qflash_forward_window, qkv_int8
 
 try:  # pragma: no cover - timm is absent in the build image
     from timm.layers import to_2tuple, trunc_normal_
@@ -56,10 +56,32 @@ class QAttention(nn.Module):
         self.head_dim = dim // num_heads
         self.qkv = nn.Linear(dim, dim * 3, bias=qkv_bias)
         self.proj = nn.Linear(dim, dim)
+        self.int8_proj = False  # set_int8_proj: the qkv projection on int8 MFMA (not in the reference)
+
+    def set_int8_proj(self, enabled: bool = True) -> "QAttention":
+        """Opt in to the int8 QKV projection fused with the quantiser
+        (qkv_int8): the qkv weight as per-channel int8 codes (taken from the
+        weight now; call again after changing it), the activations quantised
+        per tensor, the projection on int8 MFMA, the attention's int8 codes
+        straight from its epilogue.  An approximation of the fp32 projection
+        the reference computes; off by default.  Needs fp32 CUDA activations
+        with C and 3C multiples of 32 and 96; other inputs take the fp32 path."""
+        self.int8_proj = enabled
+        if enabled:
+            w8, w_scale = int8_weights(self.qkv.weight)
+            self.register_buffer("qkv_w8", w8, persistent=False)
+            self.register_buffer("qkv_w_scale", w_scale, persistent=False)
+        return self
 
     def forward(self, x: torch.Tensor, attn_mask: Optional[torch.Tensor] = None,
                 is_causal: bool = False) -> torch.Tensor:
         B, N, C = x.shape
+        if self.int8_proj and x.is_cuda and x.dtype == torch.float32 and C % 32 == 0 \
+                and self.qkv.weight.device == x.device:
+            q8, k8, v8, scales = qkv_int8(x, self.qkv_w8, self.qkv_w_scale,
+                                          None if self.qkv.bias is None else self.qkv.bias.detach(), self.num_heads)
+            x = forward_codes(q8, k8, v8, scales, attn_mask, (1.0 / self.head_dim ** 0.5) * LOG2E)
+            return self.proj(x.transpose(1, 2).reshape(B, N, C))
         qkv = self.qkv(x).reshape(B, N, 3, self.num_heads, self.head_dim).permute(2, 0, 3, 1, 4)
         q, k, v = qkv.unbind(0)           # (B, H, N, hd) views, token-major in memory
         x = qflash.forward(q, k, v, attn_mask=attn_mask)

@@ -549,6 +549,146 @@ static uint32_t* scratch_ptr(int dev) {
     return static_cast<uint32_t*>(a);
 }
 
+
+// ---- int8 QKV projection fused with the quantiser (qflash_hip_qkv_int8) -----
+// acc = x8 . w8^T on int8 MFMA (exact int32), y = RN(RN(fp32(acc) * RN(s_x *
+// s_w[c])) + b[c]) per output channel c, and of y's three column thirds (q, k,
+// v) the per-tensor scales and int8 codes exactly as qflash_hip_scales /
+// qflash_hip_quantize would compute them from a materialised fp32 y.  y is
+// never written: pass 0 reduces its absmax into the scales workspace, the
+// scales kernel forms the scales, pass 1 recomputes y and stores the codes.
+typedef int32_t pi32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t pi32x16 __attribute__((ext_vector_type(16)));
+constexpr int kProjTile = 128;  // rows (tokens) and columns (output channels) per workgroup
+
+struct ProjArgs {
+    const int8_t* x8;
+    const int8_t* w8;
+    const float* w_scale;
+    const float* bias;
+    const float* x_scale;
+    int32_t M, K, Nc, C;  // C = Nc / 3, the columns of each of q, k, v
+    uint32_t* ws;
+    const float* scales;
+    int8_t* out;
+};
+
+// 16 bytes at byte offset `off` of a buffer; past its end they read as 0
+__device__ __forceinline__ pi32x4 proj_load(__amdgpu_buffer_rsrc_t r, int32_t off) {
+    return __builtin_bit_cast(pi32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// One workgroup: a 128 x 128 tile of y, four waves of 64 x 64 (2 x 2 blocks of
+// v_mfma_i32_32x32x32_i8: lane l holds row l % 32 of x8 and of w8, 16 bytes of
+// each 32-byte K block's half l / 32; result register v of lane l is row
+// 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32).  Rows >= M and columns >= Nc
+// read as 0 (buffer range) and take no part in the results.
+// RN(RN(a * b) + c): the product and the sum rounded each (hipcc contracts
+// a * b + c into one fused multiply-add unless told not to)
+__device__ inline float mul_add_rn(float a, float b, float c) {
+#pragma clang fp contract(off)
+    return a * b + c;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256) void proj_kernel(ProjArgs p) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lr = lane & 31, g = lane >> 5;
+    const int m0 = blockIdx.x * kProjTile + (wave & 1) * 64;
+    const int n0 = blockIdx.y * kProjTile + (wave >> 1) * 64;
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)p.x8, 0, p.M * p.K, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)p.w8, 0, p.Nc * p.K, 0x00020000);
+    int32_t ao[2], bo[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        ao[i] = (m0 + 32 * i + lr) * p.K + 16 * g;
+        bo[i] = (n0 + 32 * i + lr) * p.K + 16 * g;
+    }
+    pi32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = pi32x16{};
+    pi32x4 a[2], b[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        a[i] = proj_load(rx, ao[i]);
+        b[i] = proj_load(rw, bo[i]);
+    }
+    for (int k0 = 0; k0 < p.K; k0 += 32) {
+        pi32x4 an[2], bn[2];
+        const bool more = k0 + 32 < p.K;
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                an[i] = proj_load(rx, ao[i] + k0 + 32);
+                bn[i] = proj_load(rw, bo[i] + k0 + 32);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                a[i] = an[i];
+                b[i] = bn[i];
+            }
+        }
+    }
+    const float sx = *p.x_scale;
+    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc((void*)p.out, 0, MODE == 1 ? p.M * p.Nc : 0,
+                                                                       0x00020000);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int nb = n0 + 32 * j;  // the column block (32 | C: one of q, k, v)
+        if (nb >= p.Nc) break;       // uniform over the wave
+        const int n = nb + lr;
+        const int t = nb / p.C;
+        const float gsc = sx * p.w_scale[n];
+        const float bb = p.bias ? p.bias[n] : 0.0f;
+        uint32_t mx = 0;
+        float s = 0.f, rcp = 0.f;
+        bool rcp_ok = false;
+        if constexpr (MODE == 1) {
+            s = p.scales[t];
+            rcp = __frcp_rn(s);
+            rcp_ok = s >= 0x1p-126f && s < 0x1p126f;
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int m = m0 + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3);
+                const float y = p.bias ? mul_add_rn((float)acc[i][j][v], gsc, bb) : (float)acc[i][j][v] * gsc;
+                if constexpr (MODE == 0) {
+                    if (m < p.M) mx = max(mx, __float_as_uint(y) & 0x7fffffffu);
+                } else {
+                    const int8_t c = rcp_ok ? quant1_rcp(y, s, rcp) : quant1<QFLASH_HIP_F32>(y, s);
+                    // rows >= M lie past the buffer's end: the store is dropped
+                    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)c, ro, m * p.Nc + n, 0, 0);
+                }
+            }
+        }
+        if constexpr (MODE == 0) {
+            mx = wave_max(mx);
+            if (lane == 0) atomicMax(p.ws + t * kSlots + (blockIdx.x + blockIdx.y * gridDim.x) % kSlots, mx);
+        }
+    }
+}
+
+static int qkv_int8(const ProjArgs& pa, float* scales, hipStream_t st) {
+    const dim3 grid((unsigned)((pa.M + kProjTile - 1) / kProjTile), (unsigned)((pa.Nc + kProjTile - 1) / kProjTile));
+    hipLaunchKernelGGL((proj_kernel<0>), grid, dim3(256), 0, st, pa);
+    hipLaunchKernelGGL((scales_kernel<QFLASH_HIP_F32>), dim3(1), dim3(64), 0, st, pa.ws, (void*)scales);
+    ProjArgs p1 = pa;
+    p1.scales = scales;
+    hipLaunchKernelGGL((proj_kernel<1>), grid, dim3(256), 0, st, p1);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : fail(QFLASH_HIP_ELAUNCH, "launch failed: %s", hipGetErrorString(e));
+}
+
 static int esize_of(int32_t dtype) {
     return dtype == QFLASH_HIP_F32 ? 4 : (dtype == QFLASH_HIP_F16 || dtype == QFLASH_HIP_BF16 ? 2 : 0);
 }
@@ -579,6 +719,24 @@ int qflash_hip_scales(const void* q, const void* k, const void* v, int32_t dtype
         case QFLASH_HIP_F16: return qfq::scales_dt<QFLASH_HIP_F16>(g, scales, workspace, st);
         default: return qfq::scales_dt<QFLASH_HIP_BF16>(g, scales, workspace, st);
     }
+}
+
+int qflash_hip_qkv_int8(const int8_t* x8, const int8_t* w8, const float* w_scale, const float* bias,
+                        const float* x_scale, int32_t M, int32_t K, int32_t Nc, float* scales, int8_t* codes,
+                        uint32_t* workspace, int64_t workspace_elems, void* stream) {
+    qfq::g_err[0] = 0;
+    if (!x8 || !w8 || !w_scale || !x_scale || !scales || !codes || !workspace)
+        return qfq::fail(QFLASH_HIP_EINVAL, "null pointer argument");
+    if (M < 1 || K < 32 || K % 32 || Nc < 96 || Nc % 96)
+        return qfq::fail(QFLASH_HIP_EINVAL, "shape M=%d K=%d Nc=%d: need M >= 1, K a multiple of 32, Nc = 3 C with C a "
+                         "multiple of 32", M, K, Nc);
+    if ((int64_t)M * K > INT32_MAX - 64 || (int64_t)Nc * K > INT32_MAX - 64 || (int64_t)(M + 127) * Nc > INT32_MAX)
+        return qfq::fail(QFLASH_HIP_EINVAL, "operands beyond 2 GiB");
+    if (workspace_elems < QFLASH_HIP_SCALES_WORKSPACE)
+        return qfq::fail(QFLASH_HIP_EINVAL, "workspace holds %lld entries, %d needed", (long long)workspace_elems,
+                         QFLASH_HIP_SCALES_WORKSPACE);
+    const qfq::ProjArgs pa = {x8, w8, w_scale, bias, x_scale, M, K, Nc, Nc / 3, workspace, nullptr, codes};
+    return qfq::qkv_int8(pa, scales, (hipStream_t)stream);
 }
 
 int qflash_hip_scales_noalloc(const void* q, const void* k, const void* v, int32_t dtype,

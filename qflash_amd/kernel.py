@@ -590,22 +590,77 @@ def _forward_device(query: Tensor, key: Tensor, value: Tensor, attn_mask: Tensor
                     return_mode: str):
     """qflash_forward on the device: scales, constants, quantisation, bias,
     attention with the dequantisation fused, in stream order."""
-    Z, H, N = query.shape[0], query.shape[1], query.shape[2]
     scales, finish = quantize_qkv(query, key, value)           # kernel.py:294-296
     # the quantisation needs only the scales: queued first, so that the device
     # never waits for the host's later launches
     q8, k8, v8 = finish()                                       # kernel.py:309-311
-    params = device_constants(scales, scale, N, query.shape[-1], attn_mask is not None)  # kernel.py:297-307
+    return forward_codes(q8, k8, v8, scales, attn_mask, scale, return_mode)
+
+
+def forward_codes(q8: Tensor, k8: Tensor, v8: Tensor, scales: Tensor, attn_mask: Tensor | None, scale: float,
+                  return_mode: str = 'output'):
+    """The device forward from int8 codes and their device scales (q_scale,
+    k_scale, o_scale, q_scale * k_scale, as quantize_qkv returns them):
+    constants, bias, attention with the dequantisation fused (kernel.py:297-351).
+    `scale` is the host's (scale or 1/sqrt(D)) * LOG2E."""
+    Z, H, N = q8.shape[0], q8.shape[1], q8.shape[2]
+    params = device_constants(scales, scale, N, q8.shape[-1], attn_mask is not None)  # kernel.py:297-307
     check = _status_check(params)
     bias = None if attn_mask is None else mask_to_bias_planned(attn_mask, params, Z, H, N)  # kernel.py:327-336
     if return_mode == 'latency':  # the kernel alone, int8 codes out (kernel.py:348-349)
         check()
         o = torch.empty_like(v8)
-        return bench_latency_ms(lambda: launch_forward_planned(q8, k8, v8, o, params, bias), device=query.device)
+        return bench_latency_ms(lambda: launch_forward_planned(q8, k8, v8, o, params, bias), device=q8.device)
     out = torch.empty_like(v8, dtype=scales.dtype)              # o * o_scale fused (kernel.py:351)
     launch_forward_planned(q8, k8, v8, out, params, bias, o_scale=scales[2])
     check()
     return out
+
+
+def int8_weights(weight: Tensor) -> tuple[Tensor, Tensor]:
+    """Per-output-channel int8 codes of a projection weight (Nc x K) for
+    qkv_int8: w_scale = amax|W[c, :]| / 127 in fp32 (1 for all-zero rows) and
+    w8 = clamp(rint(W / w_scale), -128, 127)."""
+    w = weight.detach().to(torch.float32)
+    w_scale = w.abs().amax(dim=1) / INT8_MAX
+    w_scale = torch.where(w_scale > 0, w_scale, torch.ones_like(w_scale))
+    w8 = torch.clamp(torch.round(w / w_scale[:, None]), -128, 127).to(torch.int8)
+    return w8.contiguous(), w_scale.contiguous()
+
+
+def qkv_int8(x: Tensor, w8: Tensor, w_scale: Tensor, bias: Tensor | None, num_heads: int):
+    """The int8 QKV projection fused with the quantiser (qflash_hip_qkv_int8).
+
+    x: (B, N, C) fp32 activations on the device; w8 / w_scale from int8_weights
+    of the (3C, C) qkv weight; bias: (3C,) fp32 or None.  The activations are
+    quantised per tensor (quantize_qkv's arithmetic), the projection runs on
+    int8 MFMA, and its q, k, v thirds come back as int8 codes with their
+    per-tensor scales, exactly as quantize_qkv would quantise a materialised
+    fp32 projection y = RN(RN(fp32(x8 . w8^T) * RN(x_scale * w_scale)) + bias).
+    Returns (q8, k8, v8, scales): (B, H, N, D) token-major views of one
+    (B, N, 3, H, D) code buffer, and the 4 fp32 scales."""
+    B, N, C = x.shape
+    if x.dtype != torch.float32 or not x.is_cuda:
+        raise ValueError("qkv_int8: fp32 activations on a GPU device")
+    M = B * N
+    x4 = x.reshape(1, 1, M, C)
+    one = x4.reshape(-1)[:1].view(1, 1, 1, 1)  # stand-ins for the key / value slots of the quantiser
+    x_scales, finish = quantize_qkv(x4, one, one)
+    x8 = finish()[0]
+    ws = _scales_workspace(x.device)
+    scales = torch.empty(4, dtype=torch.float32, device=x.device)
+    codes = torch.empty((B, N, 3, num_heads, C // num_heads), dtype=torch.int8, device=x.device)
+    L = _lib.load()
+    vp = ctypes.c_void_p
+    rc = L.qflash_hip_qkv_int8(vp(x8.data_ptr()), vp(w8.data_ptr()), vp(w_scale.data_ptr()),
+                               vp(0 if bias is None else bias.data_ptr()), vp(x_scales.data_ptr()), M, C, 3 * C,
+                               vp(scales.data_ptr()), vp(codes.data_ptr()), vp(ws.data_ptr()), ws.numel(),
+                               _stream_ptr(x))
+    if rc != 0:
+        _drop_scales_workspace(x.device)
+    _lib.check(rc, "qflash_hip_qkv_int8")
+    q8, k8, v8 = codes.permute(2, 0, 3, 1, 4).unbind(0)
+    return q8, k8, v8, scales
 
 
 def qflash_forward_window(query: Tensor, key: Tensor, value: Tensor, rel_bias: Tensor, mask: Tensor | None = None,
