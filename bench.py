@@ -357,7 +357,7 @@ def e2e_call(w, dev):
     return call
 
 
-def e2e_graph_us(w, dev, reps: int = 20) -> float:
+def e2e_graph_us(w, dev, reps: int = 20, settle_ms: float = 60.0) -> float:
     """Median time of one replay of e2e_call captured in a HIP graph (HIP events
     around each replay): the whole op with no host work between its kernels,
     possible because the constants are formed on the device."""
@@ -374,8 +374,7 @@ def e2e_graph_us(w, dev, reps: int = 20) -> float:
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         call()
-    for _ in range(3):
-        graph.replay()
+    settle(graph.replay, settle_ms)  # clocks at their loaded state, as for the kernel lines
     torch.cuda.synchronize()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
@@ -387,13 +386,12 @@ def e2e_graph_us(w, dev, reps: int = 20) -> float:
     return statistics.median(a.elapsed_time(b) for a, b in zip(starts, ends)) * 1e3
 
 
-def e2e_us(w, dev, reps: int = 10) -> float:
+def e2e_us(w, dev, reps: int = 10, settle_ms: float = 60.0) -> float:
     """Median wall time of e2e_call, host sync included."""
     import torch
 
     call = e2e_call(w, dev)
-    call()
-    torch.cuda.synchronize()
+    settle(call, settle_ms)
     times = []
     for _ in range(reps):
         t = time.perf_counter()

@@ -1530,15 +1530,31 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
 }
 
 // The kernels on constants in device memory (qflash_hip_constants), for
-// layouts the fast kernel accepts: the plan selects the fast path (and, by
-// the identity proof of the rescale, id_ok, one of its two variants) or the
-// general one, in one launch.
+// layouts the fast kernel accepts.  Two launches on the same grid, each
+// returning at once unless the plan selects it: fwd_fast_planned runs the fast
+// path when the plan proves the rescale by rs the identity (id_ok, the common
+// case), fwd_planned_rest every other plan (the per-row bound variant, or the
+// general path).  One kernel holding every path keeps the plan's values in
+// scalar registers across all of them and spills them to vector lanes in the
+// hot loop (cfg3 90.5 us against 82.3 us for the one-path kernel); an empty
+// launch costs ~2.5 us.
 template <int D, int W, bool MASKED>
 __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast_planned(Args a) {
     using S = Stage<D, W>;
+    __shared__ __attribute__((aligned(16))) int8_t smem[2 * S::BYTES + kLutMax];
+    if (a.params[kPStatus] != 0 || !a.params[kPFast] || !a.params[kPIdOk]) return;
+    load_params(a);
+    fill_lut<W, MASKED>(a, smem + 2 * S::BYTES);
+    const int wg = xcd_order(blockIdx.x, a.n_wg);
+    fast_block<D, W, MASKED, false>(a, smem, wg / a.mblocks, wg % a.mblocks);
+}
+
+template <int D, int W, bool MASKED>
+__global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_planned_rest(Args a) {
+    using S = Stage<D, W>;
     static_assert(Tile<D>::BYTES <= 2 * S::BYTES + kLutMax, "the general path's tiles fit the fast path's LDS");
     __shared__ __attribute__((aligned(16))) int8_t smem[2 * S::BYTES + kLutMax];
-    if (a.params[kPStatus] != 0) return;
+    if (a.params[kPStatus] != 0 || (a.params[kPFast] && a.params[kPIdOk])) return;
     load_params(a);
     if (!a.params[kPFast]) {
         general_block<D, W, MASKED, true>(a, xcd_order(blockIdx.x, a.n_wg), smem);
@@ -1546,10 +1562,7 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast_pla
     }
     fill_lut<W, MASKED>(a, smem + 2 * S::BYTES);
     const int wg = xcd_order(blockIdx.x, a.n_wg);
-    if (a.id_ok)
-        fast_block<D, W, MASKED, false>(a, smem, wg / a.mblocks, wg % a.mblocks);
-    else
-        fast_block<D, W, MASKED, true>(a, smem, wg / a.mblocks, wg % a.mblocks);
+    fast_block<D, W, MASKED, true>(a, smem, wg / a.mblocks, wg % a.mblocks);
 }
 
 
@@ -1618,11 +1631,15 @@ static hipError_t launch_fast(const Args& a, int wg_per_cu, dim3 grid, hipStream
 template <int D, int W, bool MASKED>
 static hipError_t launch_dw(const Args& a, bool vec, bool fast, int wg_per_cu, dim3 grid, hipStream_t st) {
     if (a.params) {
-        // constants in device memory: one kernel whose path the plan selects when
-        // the layout admits the fast kernel, the general kernel otherwise
+        // constants in device memory: the two planned kernels (the plan selects
+        // one of them) when the layout admits the fast kernel, the general
+        // kernel otherwise
         if constexpr (D <= 128) {
             if (fast) {
                 hipLaunchKernelGGL((fwd_fast_planned<D, W, MASKED>), grid, dim3(64 * W), 0, st, a);
+                const hipError_t e = hipGetLastError();
+                if (e != hipSuccess) return e;
+                hipLaunchKernelGGL((fwd_planned_rest<D, W, MASKED>), grid, dim3(64 * W), 0, st, a);
                 return hipGetLastError();
             }
         }

@@ -393,14 +393,17 @@ def _flag_kw():
                 L_SHIFT=L_SHIFT, ACC_SHIFT=ACC_SHIFT)
 
 
-def device_constants(scales: Tensor, scale: float, N: int, D: int, masked: bool) -> Tensor:
+def device_constants(scales: Tensor, scale: float, N: int, D: int, masked: bool,
+                     params: Tensor | None = None) -> Tensor:
     """The fixed-point constants on the device (qflash_hip_constants): a device
     int32 block of _lib.PARAMS_WORDS words holding a status (0, or the
     exception the reference's host would raise, see raise_status), sm_rscale,
     exp_M, req_M, l_M, acc_M (kernel.py:297-307, Python's double arithmetic),
     the fast kernel's plan and sm_scale.  `scales` from quantize_qkv; `scale`
-    the host's (scale or 1/sqrt(D)) * LOG2E.  Asynchronous, no host sync."""
-    params = torch.empty(_lib.PARAMS_WORDS, dtype=torch.int32, device=scales.device)
+    the host's (scale or 1/sqrt(D)) * LOG2E; `params`: the block to write (a
+    new one when None).  Asynchronous, no host sync."""
+    if params is None:
+        params = torch.empty(_lib.PARAMS_WORDS, dtype=torch.int32, device=scales.device)
     fl = _flags()
     _lib.check(_lib.load().qflash_hip_constants(ctypes.c_void_p(scales.data_ptr()), _DT_CODE[scales.dtype],
                                                 float(scale), int(N), int(D), int(masked), ctypes.byref(fl),
@@ -449,6 +452,25 @@ def _status_check(params: Tensor):
             wait = _scalar_to_host(params[0])
         raise_status(int(wait()))
     return check
+
+
+def _constants_beside(scales: Tensor, scale: float, N: int, D: int, masked: bool, then=None):
+    """device_constants queued on this thread's side stream after the work
+    already queued on the current one (the scales), so that the one-wave
+    constants kernel runs while the current stream's quantisation pass does;
+    `then(params)`, if given, is queued after it on the side stream too.
+    Returns (params, then's result, join); join() makes the current stream wait
+    for the side stream (call it before anything reads params)."""
+    main = torch.cuda.current_stream(scales.device)
+    side = _side_stream(scales.device)
+    params = torch.empty(_lib.PARAMS_WORDS, dtype=torch.int32, device=scales.device)  # owned by `main`
+    side.wait_stream(main)
+    with torch.cuda.stream(side):
+        device_constants(scales, scale, N, D, masked, params)
+        extra = then(params) if then is not None else None
+    if isinstance(extra, Tensor):
+        extra.record_stream(main)  # allocated on `side`, read on `main`
+    return params, extra, lambda: main.wait_stream(side)
 
 
 def _side_stream(device) -> torch.cuda.Stream:
@@ -591,20 +613,24 @@ def _forward_device(query: Tensor, key: Tensor, value: Tensor, attn_mask: Tensor
     """qflash_forward on the device: scales, constants, quantisation, bias,
     attention with the dequantisation fused, in stream order."""
     scales, finish = quantize_qkv(query, key, value)           # kernel.py:294-296
-    # the quantisation needs only the scales: queued first, so that the device
-    # never waits for the host's later launches
+    # the constants need only the scales: on a side stream, beside the quantisation
+    params, _, join = _constants_beside(scales, scale, query.shape[2], query.shape[-1],
+                                        attn_mask is not None)  # kernel.py:297-307
     q8, k8, v8 = finish()                                       # kernel.py:309-311
-    return forward_codes(q8, k8, v8, scales, attn_mask, scale, return_mode)
+    join()
+    return forward_codes(q8, k8, v8, scales, attn_mask, scale, return_mode, params=params)
 
 
 def forward_codes(q8: Tensor, k8: Tensor, v8: Tensor, scales: Tensor, attn_mask: Tensor | None, scale: float,
-                  return_mode: str = 'output'):
+                  return_mode: str = 'output', params: Tensor | None = None):
     """The device forward from int8 codes and their device scales (q_scale,
     k_scale, o_scale, q_scale * k_scale, as quantize_qkv returns them):
     constants, bias, attention with the dequantisation fused (kernel.py:297-351).
-    `scale` is the host's (scale or 1/sqrt(D)) * LOG2E."""
+    `scale` is the host's (scale or 1/sqrt(D)) * LOG2E; `params`: the constants
+    already queued for these scales (device_constants), or None."""
     Z, H, N = q8.shape[0], q8.shape[1], q8.shape[2]
-    params = device_constants(scales, scale, N, q8.shape[-1], attn_mask is not None)  # kernel.py:297-307
+    if params is None:
+        params = device_constants(scales, scale, N, q8.shape[-1], attn_mask is not None)  # kernel.py:297-307
     check = _status_check(params)
     bias = None if attn_mask is None else mask_to_bias_planned(attn_mask, params, Z, H, N)  # kernel.py:327-336
     if return_mode == 'latency':  # the kernel alone, int8 codes out (kernel.py:348-349)
@@ -687,10 +713,13 @@ def qflash_forward_window(query: Tensor, key: Tensor, value: Tensor, rel_bias: T
         if mask is not None and Z % mask.shape[0]:
             raise ValueError(f"batch {Z} is not a multiple of the {mask.shape[0]} windows of the mask")
         scales, finish = quantize_qkv(query, key, value)
+        # the constants and the window bias need only the scales: on a side
+        # stream, beside the quantisation
+        params, wb, join = _constants_beside(scales, scale, N, d_q, True,
+                                             lambda p: window_bias_planned(rel_bias, mask, p))
         q8, k8, v8 = finish()
-        params = device_constants(scales, scale, N, d_q, True)
+        join()
         check = _status_check(params)
-        wb = window_bias_planned(rel_bias, mask, params)
         bias, zmod = (wb.expand(Z, H, N, N), 0) if mask is None else (wb, mask.shape[0])
         out = torch.empty_like(v8, dtype=scales.dtype)
         launch_forward_planned(q8, k8, v8, out, params, bias, zmod, o_scale=scales[2])
