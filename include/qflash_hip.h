@@ -243,6 +243,18 @@ int qflash_hip_constants(const void* scales, int32_t dtype, double scale, int32_
                          int32_t masked, const qflash_hip_flags* flags, int32_t* params, void* stream);
 
 /*
+ * qflash_hip_scales followed by qflash_hip_constants (qflash/kernel.py:294-307),
+ * in two launches instead of three: the absmax pass, then one one-wave kernel
+ * that forms the scales and, from scales[3] as stored in `dtype`, the
+ * constants and plan.  Arguments, workspace contract and results are those of
+ * the two calls.  Allocates nothing.
+ */
+int qflash_hip_scales_constants(const void* q, const void* k, const void* v, int32_t dtype,
+                                const int64_t* shapes_strides, void* scales, uint32_t* workspace,
+                                int64_t workspace_elems, double scale, int32_t N_CTX, int32_t HEAD_DIM, int32_t masked,
+                                const qflash_hip_flags* flags, int32_t* params, void* stream);
+
+/*
  * qflash_hip_forward with the constants in device memory (`params` from
  * qflash_hip_constants with the same N_CTX, HEAD_DIM, masking and flags)
  * instead of host integers.  No counterpart in the reference.  Nothing is

@@ -33,6 +33,7 @@ class Flags(ctypes.Structure):
 EXPORTS = ("qflash_hip_kernel", "qflash_hip_masked_kernel", "qflash_hip_window_kernel", "qflash_hip_forward",
            "qflash_hip_scales", "qflash_hip_scales_noalloc", "qflash_hip_qkv_int8",
            "qflash_hip_quantize", "qflash_hip_window_bias", "qflash_hip_mask_bias", "qflash_hip_constants",
+           "qflash_hip_scales_constants",
            "qflash_hip_forward_planned", "qflash_hip_window_bias_planned", "qflash_hip_mask_bias_planned",
            "qflash_hip_last_error",
            "qflash_hip_mfma_layout_check", "qflash_hip_lut_bounds", "qflash_hip_far_bounds",
@@ -79,6 +80,9 @@ def _declare(L):
     L.qflash_hip_mask_bias.argtypes = [vp, ctypes.c_int64, ctypes.c_double, vp, vp]
     L.qflash_hip_constants.restype = ctypes.c_int
     L.qflash_hip_constants.argtypes = [vp, i32, ctypes.c_double, i32, i32, i32, fp, vp, vp]
+    L.qflash_hip_scales_constants.restype = ctypes.c_int
+    L.qflash_hip_scales_constants.argtypes = [vp, vp, vp, i32, i64p, vp, vp, ctypes.c_int64, ctypes.c_double, i32, i32,
+                                              i32, fp, vp, vp]
     L.qflash_hip_forward_planned.restype = ctypes.c_int
     L.qflash_hip_forward_planned.argtypes = [vp, vp, vp, vp, i32, vp, vp, i32, vp, i64p, i32, i32, i32, i32, fp, vp]
     L.qflash_hip_window_bias_planned.restype = ctypes.c_int

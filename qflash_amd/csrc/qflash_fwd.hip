@@ -263,13 +263,11 @@ __device__ static int device_constants(double sm, int l_shift, int acc_shift, in
     return 0;
 }
 
-// One wave: lane 0 forms the constants and the plan; the table scan of
-// lut_bounds runs over the lanes.
-__global__ __launch_bounds__(64) void constants_kernel(const void* scales, int32_t dt, double scale, Args a,
-                                                       int32_t masked, uint32_t hooks, int32_t* params) {
+// One wave: the constants and the plan from sm = scale * float(q_scale *
+// k_scale); the table scan of lut_bounds runs over the lanes, lane 0 writes
+// the parameter block.
+__device__ static void constants_body(double sm, Args a, int32_t masked, uint32_t hooks, int32_t* params) {
     const int lane = threadIdx.x;
-    const double sm = scale * scale_value_f64(static_cast<const char*>(scales) + 3 * (dt == QFLASH_HIP_F32 ? 4 : 2),
-                                              dt);
     int32_t c[5] = {0, 0, 0, 0, 0};
     const int status = device_constants(sm, a.l_shift, a.acc_shift, c);
     a.rs = c[0]; a.eM = c[1]; a.rM = c[2]; a.lM = c[3]; a.aM = c[4];
@@ -307,6 +305,49 @@ __global__ __launch_bounds__(64) void constants_kernel(const void* scales, int32
         w[kPSmScale + 1] = (int32_t)(uint32_t)(smb >> 32);
         for (int i = 0; i < QFLASH_HIP_PARAMS_WORDS; ++i) params[i] = w[i];
     }
+}
+
+__global__ __launch_bounds__(64) void constants_kernel(const void* scales, int32_t dt, double scale, Args a,
+                                                       int32_t masked, uint32_t hooks, int32_t* params) {
+    const double sm = scale * scale_value_f64(static_cast<const char*>(scales) + 3 * (dt == QFLASH_HIP_F32 ? 4 : 2),
+                                              dt);
+    constants_body(sm, a, masked, hooks, params);
+}
+
+// The scales kernel of qflash_hip_scales and constants_kernel in one wave:
+// the scales from the absmax slots (which it sets back to zero), then the
+// constants from their product as stored in T.
+template <int DT>
+__global__ __launch_bounds__(64) void scales_constants_kernel(uint32_t* ws, void* scales, double scale, Args a,
+                                                              int32_t masked, uint32_t hooks, int32_t* params) {
+    const float qk = qfs::reduce_scale_slots<DT>(ws, scales);
+    constants_body(scale * (double)qk, a, masked, hooks, params);
+}
+
+// Checks of qflash_hip_constants' arguments and the Args fields its kernel
+// reads; *hooks: the test-hook bits of this call.
+static int constants_args(int32_t dtype, int32_t N, int32_t D, const qflash_hip_flags* flags, const int32_t* params,
+                          Args* a, uint32_t* hooks) {
+    if (!params) return fail(QFLASH_HIP_EINVAL, "null pointer argument");
+    if (dtype != QFLASH_HIP_F32 && dtype != QFLASH_HIP_F16 && dtype != QFLASH_HIP_BF16)
+        return fail(QFLASH_HIP_EINVAL, "unknown dtype code %d", dtype);
+    if (N <= 0 || D <= 0) return fail(QFLASH_HIP_EINVAL, "bad N_CTX=%d HEAD_DIM=%d", N, D);
+    if (((uintptr_t)params & 7u) != 0) return fail(QFLASH_HIP_EINVAL, "params must be 8-byte aligned");
+    qflash_hip_flags f = {1, 1, 1, 30, 30};
+    if (flags) f = *flags;
+    if (f.l_use_shift && (f.l_shift < 1 || f.l_shift > 62))
+        return fail(QFLASH_HIP_EINVAL, "l_shift %d outside 1..62", f.l_shift);
+    if (f.acc_use_shift && (f.acc_shift < 1 || f.acc_shift > 62))
+        return fail(QFLASH_HIP_EINVAL, "acc_shift %d outside 1..62", f.acc_shift);
+    a->N = N;
+    a->l_shift = f.l_shift;
+    a->acc_shift = f.acc_shift;
+    a->exp_mode = f.exp_use_shift != 0;
+    a->l_mode = f.l_use_shift != 0;
+    a->acc_mode = f.acc_use_shift != 0;
+    *hooks = g_hook_bits.load(std::memory_order_relaxed);
+    a->force_robust = (*hooks & QFLASH_HIP_HOOK_FORCE_ROBUST) ? 1 : 0;
+    return 0;
 }
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -464,28 +505,43 @@ int qflash_hip_forward(const int8_t* Q, const int8_t* K, const int8_t* V, void* 
 int qflash_hip_constants(const void* scales, int32_t dtype, double scale, int32_t N_CTX, int32_t HEAD_DIM,
                          int32_t masked, const qflash_hip_flags* flags, int32_t* params, void* stream) {
     qf::g_err[0] = 0;
-    if (!scales || !params) return qf::fail(QFLASH_HIP_EINVAL, "null pointer argument");
-    if (dtype != QFLASH_HIP_F32 && dtype != QFLASH_HIP_F16 && dtype != QFLASH_HIP_BF16)
-        return qf::fail(QFLASH_HIP_EINVAL, "unknown dtype code %d", dtype);
-    if (N_CTX <= 0 || HEAD_DIM <= 0) return qf::fail(QFLASH_HIP_EINVAL, "bad N_CTX=%d HEAD_DIM=%d", N_CTX, HEAD_DIM);
-    if (((uintptr_t)params & 7u) != 0) return qf::fail(QFLASH_HIP_EINVAL, "params must be 8-byte aligned");
-    qflash_hip_flags f = {1, 1, 1, 30, 30};
-    if (flags) f = *flags;
-    if (f.l_use_shift && (f.l_shift < 1 || f.l_shift > 62))
-        return qf::fail(QFLASH_HIP_EINVAL, "l_shift %d outside 1..62", f.l_shift);
-    if (f.acc_use_shift && (f.acc_shift < 1 || f.acc_shift > 62))
-        return qf::fail(QFLASH_HIP_EINVAL, "acc_shift %d outside 1..62", f.acc_shift);
+    if (!scales) return qf::fail(QFLASH_HIP_EINVAL, "null pointer argument");
     qf::Args a{};
-    a.N = N_CTX;
-    a.l_shift = f.l_shift;
-    a.acc_shift = f.acc_shift;
-    a.exp_mode = f.exp_use_shift != 0;
-    a.l_mode = f.l_use_shift != 0;
-    a.acc_mode = f.acc_use_shift != 0;
-    const uint32_t hooks = qf::g_hook_bits.load(std::memory_order_relaxed);
-    a.force_robust = (hooks & QFLASH_HIP_HOOK_FORCE_ROBUST) ? 1 : 0;
+    uint32_t hooks = 0;
+    if (int rc = qf::constants_args(dtype, N_CTX, HEAD_DIM, flags, params, &a, &hooks)) return rc;
     hipLaunchKernelGGL(qf::constants_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, scales, dtype, scale, a,
                        masked ? 1 : 0, hooks, params);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return qf::fail(QFLASH_HIP_ELAUNCH, "launch failed: %s", hipGetErrorString(e));
+    return QFLASH_HIP_OK;
+}
+
+int qflash_hip_scales_constants(const void* q, const void* k, const void* v, int32_t dtype,
+                                const int64_t* shapes_strides, void* scales, uint32_t* workspace,
+                                int64_t workspace_elems, double scale, int32_t N_CTX, int32_t HEAD_DIM, int32_t masked,
+                                const qflash_hip_flags* flags, int32_t* params, void* stream) {
+    qf::g_err[0] = 0;
+    if (!scales) return qf::fail(QFLASH_HIP_EINVAL, "null pointer argument");
+    qf::Args a{};
+    uint32_t hooks = 0;
+    if (int rc = qf::constants_args(dtype, N_CTX, HEAD_DIM, flags, params, &a, &hooks)) return rc;
+    if (int rc = qfq::absmax_pass(q, k, v, dtype, shapes_strides, nullptr, workspace, workspace_elems, stream))
+        return rc;
+    const hipStream_t st = (hipStream_t)stream;
+    const int32_t mk = masked ? 1 : 0;
+    switch (dtype) {
+        case QFLASH_HIP_F32:
+            hipLaunchKernelGGL(qf::scales_constants_kernel<QFLASH_HIP_F32>, dim3(1), dim3(64), 0, st, workspace,
+                               scales, scale, a, mk, hooks, params);
+            break;
+        case QFLASH_HIP_F16:
+            hipLaunchKernelGGL(qf::scales_constants_kernel<QFLASH_HIP_F16>, dim3(1), dim3(64), 0, st, workspace,
+                               scales, scale, a, mk, hooks, params);
+            break;
+        default:
+            hipLaunchKernelGGL(qf::scales_constants_kernel<QFLASH_HIP_BF16>, dim3(1), dim3(64), 0, st, workspace,
+                               scales, scale, a, mk, hooks, params);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return qf::fail(QFLASH_HIP_ELAUNCH, "launch failed: %s", hipGetErrorString(e));
     return QFLASH_HIP_OK;

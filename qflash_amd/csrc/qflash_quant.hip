@@ -34,15 +34,18 @@ namespace qfq {
 
 using qferr::fail;
 using qferr::g_err;
+using qfs::round_t;
+using qfs::store_t;
+using qfs::to_float;
+using qfs::wave_max;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
 constexpr int kSeg = 8 * kThreads;  // 16-byte chunks per work unit
-constexpr int kSlots = 64;          // atomic-max slots per tensor (spreads the contention)
+constexpr int kSlots = qfs::kScaleSlots;  // atomic-max slots per tensor (spreads the contention)
 constexpr int32_t kNegInfBias = -(1 << 20);  // qflash/kernel.py:288
-static_assert(3 * kSlots <= QFLASH_HIP_SCALES_WORKSPACE, "workspace: 3 x kSlots partial maxima");
 
 // One tensor as `rows` runs of L contiguous elements; a run's start is
 // sum_i idx_i * in_stride_i over up to 3 outer dimensions (sizes n[], the
@@ -82,31 +85,6 @@ __device__ __forceinline__ uint32_t load_raw(const void* p, int64_t i) {
     else return reinterpret_cast<const uint16_t*>(p)[i];
 }
 
-__device__ __forceinline__ uint32_t wave_max(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o));
-    return v;
-}
-
-// T value of a pattern and fp32 -> T rounding (round to nearest even).
-template <int DT>
-__device__ __forceinline__ float to_float(uint32_t bits) {
-    if constexpr (DT == QFLASH_HIP_F32) return __uint_as_float(bits);
-    else if constexpr (DT == QFLASH_HIP_F16) return __half2float(__ushort_as_half((unsigned short)bits));
-    else return __uint_as_float(bits << 16);
-}
-template <int DT>
-__device__ __forceinline__ float round_t(float f) {
-    if constexpr (DT == QFLASH_HIP_F32) return f;
-    else if constexpr (DT == QFLASH_HIP_F16) return __half2float(__float2half_rn(f));
-    else return __uint_as_float(qf_bf16_bits(f) << 16);
-}
-template <int DT>
-__device__ __forceinline__ void store_t(void* p, int i, float f) {
-    if constexpr (DT == QFLASH_HIP_F32) reinterpret_cast<float*>(p)[i] = f;
-    else if constexpr (DT == QFLASH_HIP_F16) reinterpret_cast<__half*>(p)[i] = __float2half_rn(f);
-    else reinterpret_cast<uint16_t*>(p)[i] = (uint16_t)qf_bf16_bits(f);
-}
 template <int DT>
 __device__ __forceinline__ float load_t(const void* p, int64_t i) {
     return to_float<DT>(load_raw<DT>(p, i));
@@ -155,20 +133,6 @@ __device__ __forceinline__ void run_start(const Geo& g, int64_t r, int64_t& in, 
             out += idx * g.os[i];
         }
     }
-}
-
-// q, k, v scales from the three absmax patterns, in T: torch divides a GPU
-// tensor by a host scalar as a product with the scalar's reciprocal in the
-// opmath type (fp32): amax * RN(1/127); scales[3] = scales[0] * scales[1].
-template <int DT>
-__device__ void write_scales(const uint32_t* m, void* scales) {
-    float s[3];
-#pragma unroll
-    for (int t = 0; t < 3; ++t) {
-        s[t] = round_t<DT>(to_float<DT>(m[t]) * (1.0f / 127.0f));  // kernel.py:294-296
-        store_t<DT>(scales, t, s[t]);
-    }
-    store_t<DT>(scales, 3, round_t<DT>(s[0] * s[1]));  // (q_scale * k_scale), kernel.py:297
 }
 
 // MODE 0: absmax of the patterns into ws[tensor * kSlots + block % kSlots]
@@ -330,17 +294,11 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(GeoSet gs, uint32_t* w
     }
 }
 
-// The scales from the slots of the absmax pass (one wave: lane i reads slot i
-// of each tensor), which it sets back to zero for the next call.
+// The scales from the slots of the absmax pass (one wave), which it sets back
+// to zero for the next call.
 template <int DT>
 __global__ __launch_bounds__(64) void scales_kernel(uint32_t* ws, void* scales) {
-    uint32_t m[3];
-#pragma unroll
-    for (int t = 0; t < 3; ++t) {
-        m[t] = wave_max(ws[t * kSlots + threadIdx.x]);
-        ws[t * kSlots + threadIdx.x] = 0;
-    }
-    if (threadIdx.x == 0) write_scales<DT>(m, scales);
+    qfs::reduce_scale_slots<DT>(ws, scales);
 }
 
 // Runs of a tensor in its memory order (see the file comment).  `o` / `os4`
@@ -450,12 +408,14 @@ static unsigned grid_x(const Geo* g, int es, int cpt) {
     return (unsigned)(units < cap ? units : cap);
 }
 
+// The absmax pass; then the scales kernel unless `scales` is null (the
+// caller forms the scales itself from the slots).
 template <int DT>
 static int scales_dt(Geo* g, void* scales, uint32_t* ws, hipStream_t st) {
     const dim3 grid(grid_x(g, esize<DT>(), QF_ABSMAX_CPT), 3);
     const GeoSet gs = {{g[0], g[1], g[2]}};
     hipLaunchKernelGGL((stream_kernel<DT, 0>), grid, dim3(kThreads), 0, st, gs, ws, nullptr);
-    hipLaunchKernelGGL((scales_kernel<DT>), dim3(1), dim3(64), 0, st, ws, scales);
+    if (scales) hipLaunchKernelGGL((scales_kernel<DT>), dim3(1), dim3(64), 0, st, ws, scales);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : fail(QFLASH_HIP_ELAUNCH, "launch failed: %s", hipGetErrorString(e));
 }
@@ -693,6 +653,30 @@ static int esize_of(int32_t dtype) {
     return dtype == QFLASH_HIP_F32 ? 4 : (dtype == QFLASH_HIP_F16 || dtype == QFLASH_HIP_BF16 ? 2 : 0);
 }
 
+// qflash_hip_scales, and without its scales kernel when `scales` is null.
+int absmax_pass(const void* q, const void* k, const void* v, int32_t dtype, const int64_t* shapes_strides,
+                void* scales, uint32_t* workspace, int64_t workspace_elems, void* stream) {
+    if (!q || !k || !v || !shapes_strides || !workspace)
+        return fail(QFLASH_HIP_EINVAL, "null pointer argument");
+    const int es = esize_of(dtype);
+    if (!es) return fail(QFLASH_HIP_EINVAL, "unknown dtype code %d", dtype);
+    if (workspace_elems < QFLASH_HIP_SCALES_WORKSPACE)
+        return fail(QFLASH_HIP_EINVAL, "workspace holds %lld entries, %d needed", (long long)workspace_elems,
+                         QFLASH_HIP_SCALES_WORKSPACE);
+    Geo g[3];
+    const void* x[3] = {q, k, v};
+    for (int i = 0; i < 3; ++i)
+        if (int rc = make_geo(g[i], x[i], shapes_strides + 8 * i, shapes_strides + 8 * i + 4, nullptr,
+                                   nullptr, es, i))
+            return rc;
+    hipStream_t st = (hipStream_t)stream;
+    switch (dtype) {
+        case QFLASH_HIP_F32: return scales_dt<QFLASH_HIP_F32>(g, scales, workspace, st);
+        case QFLASH_HIP_F16: return scales_dt<QFLASH_HIP_F16>(g, scales, workspace, st);
+        default: return scales_dt<QFLASH_HIP_BF16>(g, scales, workspace, st);
+    }
+}
+
 }  // namespace qfq
 
 extern "C" {
@@ -700,25 +684,8 @@ extern "C" {
 int qflash_hip_scales(const void* q, const void* k, const void* v, int32_t dtype, const int64_t* shapes_strides,
                       void* scales, uint32_t* workspace, int64_t workspace_elems, void* stream) {
     qfq::g_err[0] = 0;
-    if (!q || !k || !v || !shapes_strides || !scales || !workspace)
-        return qfq::fail(QFLASH_HIP_EINVAL, "null pointer argument");
-    const int es = qfq::esize_of(dtype);
-    if (!es) return qfq::fail(QFLASH_HIP_EINVAL, "unknown dtype code %d", dtype);
-    if (workspace_elems < QFLASH_HIP_SCALES_WORKSPACE)
-        return qfq::fail(QFLASH_HIP_EINVAL, "workspace holds %lld entries, %d needed", (long long)workspace_elems,
-                         QFLASH_HIP_SCALES_WORKSPACE);
-    qfq::Geo g[3];
-    const void* x[3] = {q, k, v};
-    for (int i = 0; i < 3; ++i)
-        if (int rc = qfq::make_geo(g[i], x[i], shapes_strides + 8 * i, shapes_strides + 8 * i + 4, nullptr,
-                                   nullptr, es, i))
-            return rc;
-    hipStream_t st = (hipStream_t)stream;
-    switch (dtype) {
-        case QFLASH_HIP_F32: return qfq::scales_dt<QFLASH_HIP_F32>(g, scales, workspace, st);
-        case QFLASH_HIP_F16: return qfq::scales_dt<QFLASH_HIP_F16>(g, scales, workspace, st);
-        default: return qfq::scales_dt<QFLASH_HIP_BF16>(g, scales, workspace, st);
-    }
+    if (!scales) return qfq::fail(QFLASH_HIP_EINVAL, "null pointer argument");
+    return qfq::absmax_pass(q, k, v, dtype, shapes_strides, scales, workspace, workspace_elems, stream);
 }
 
 int qflash_hip_qkv_int8(const int8_t* x8, const int8_t* w8, const float* w_scale, const float* bias,

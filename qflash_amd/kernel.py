@@ -275,16 +275,27 @@ def _scalar_to_host(x: Tensor):
 
 
 def _scales_workspace(device) -> Tensor:
-    """The absmax pass's workspace for this thread and device: zeroed once, and
-    left zeroed by every call when it completes (calls of one thread follow
-    each other in stream order on one device's current stream)."""
+    """The absmax pass's workspace for this thread and device's current stream:
+    zeroed once, and left zeroed by every call when it completes (calls on one
+    stream follow each other in stream order).  A stream seen for the first
+    time during HIP graph capture takes the spare workspace that an earlier
+    eager call zeroed, so that the zero fill is not captured into the graph and
+    repeated by every replay."""
     cache = getattr(_ws_cache, "d", None)
     if cache is None:
         cache = _ws_cache.d = {}
     key = (device.index, torch.cuda.current_stream(device).cuda_stream)
     ws = cache.get(key)
     if ws is None:
-        ws = cache[key] = torch.zeros(_lib.SCALES_WORKSPACE, dtype=torch.int32, device=device)
+        spare_key = (device.index, "spare")
+        if torch.cuda.is_current_stream_capturing() and spare_key in cache:
+            ws = cache[key] = cache.pop(spare_key)
+        else:
+            ws = cache[key] = torch.zeros(_lib.SCALES_WORKSPACE, dtype=torch.int32, device=device)
+    if not torch.cuda.is_current_stream_capturing() and (device.index, "spare") not in cache:
+        spare = torch.zeros(_lib.SCALES_WORKSPACE, dtype=torch.int32, device=device)
+        torch.cuda.current_stream(device).synchronize()  # once per thread and device: zero before any capture
+        cache[(device.index, "spare")] = spare
     return ws
 
 
@@ -323,19 +334,37 @@ def quantize_qkv(query: Tensor, key: Tensor, value: Tensor):
         def finish_torch():
             return quantize(query, q_scale), quantize(key, k_scale), quantize(value, o_scale)
         return scales, finish_torch
+    scales, _, finish = _hip_scales(query, key, value, None)
+    return scales, finish
+
+
+def _hip_scales(query: Tensor, key: Tensor, value: Tensor, plan):
+    """quantize_qkv's HIP path for fp32 / fp16 / bf16 (Z, H, N, D) inputs of
+    one dtype.  plan: None, or (scale, N, D, masked) of device_constants: then
+    the constants are formed in the same one-wave kernel as the scales
+    (qflash_hip_scales_constants).  Returns (scales, params or None, finish)."""
     L = _lib.load()
-    code = _DT_CODE[T]
+    code = _DT_CODE[query.dtype]
     geo = (ctypes.c_int64 * 24)(*query.shape, *query.stride(), *key.shape, *key.stride(), *value.shape,
                                  *value.stride())
     ws = _scales_workspace(query.device)
-    scales = torch.empty(4, dtype=T, device=query.device)
+    scales = torch.empty(4, dtype=query.dtype, device=query.device)
     stream = _stream_ptr(query)
     ptrs = [ctypes.c_void_p(x.data_ptr()) for x in (query, key, value)]
-    rc = L.qflash_hip_scales(*ptrs, code, geo, ctypes.c_void_p(scales.data_ptr()), ctypes.c_void_p(ws.data_ptr()),
-                             ws.numel(), stream)
+    params = None
+    if plan is None:
+        rc = L.qflash_hip_scales(*ptrs, code, geo, ctypes.c_void_p(scales.data_ptr()),
+                                 ctypes.c_void_p(ws.data_ptr()), ws.numel(), stream)
+    else:
+        scale, N, D, masked = plan
+        params = torch.empty(_lib.PARAMS_WORDS, dtype=torch.int32, device=query.device)
+        rc = L.qflash_hip_scales_constants(*ptrs, code, geo, ctypes.c_void_p(scales.data_ptr()),
+                                           ctypes.c_void_p(ws.data_ptr()), ws.numel(), float(scale), int(N), int(D),
+                                           int(masked), ctypes.byref(_flags()), ctypes.c_void_p(params.data_ptr()),
+                                           stream)
     if rc != 0:
         _drop_scales_workspace(query.device)
-    _lib.check(rc, "qflash_hip_scales")
+    _lib.check(rc, "qflash_hip_scales" if plan is None else "qflash_hip_scales_constants")
 
     def finish():
         q8, k8, v8 = (torch.empty_like(x, dtype=torch.int8) for x in (query, key, value))
@@ -345,7 +374,7 @@ def quantize_qkv(query: Tensor, key: Tensor, value: Tensor):
                                          ctypes.c_void_p(scales.data_ptr()), _stream_ptr(query)),
                    "qflash_hip_quantize")
         return q8, k8, v8
-    return scales, finish
+    return scales, params, finish
 
 
 def launch_forward(q8: Tensor, k8: Tensor, v8: Tensor, out: Tensor, consts, flags: dict, bias: Tensor | None = None,
@@ -452,25 +481,6 @@ def _status_check(params: Tensor):
             wait = _scalar_to_host(params[0])
         raise_status(int(wait()))
     return check
-
-
-def _constants_beside(scales: Tensor, scale: float, N: int, D: int, masked: bool, then=None):
-    """device_constants queued on this thread's side stream after the work
-    already queued on the current one (the scales), so that the one-wave
-    constants kernel runs while the current stream's quantisation pass does;
-    `then(params)`, if given, is queued after it on the side stream too.
-    Returns (params, then's result, join); join() makes the current stream wait
-    for the side stream (call it before anything reads params)."""
-    main = torch.cuda.current_stream(scales.device)
-    side = _side_stream(scales.device)
-    params = torch.empty(_lib.PARAMS_WORDS, dtype=torch.int32, device=scales.device)  # owned by `main`
-    side.wait_stream(main)
-    with torch.cuda.stream(side):
-        device_constants(scales, scale, N, D, masked, params)
-        extra = then(params) if then is not None else None
-    if isinstance(extra, Tensor):
-        extra.record_stream(main)  # allocated on `side`, read on `main`
-    return params, extra, lambda: main.wait_stream(side)
 
 
 def _side_stream(device) -> torch.cuda.Stream:
@@ -612,12 +622,10 @@ def _forward_device(query: Tensor, key: Tensor, value: Tensor, attn_mask: Tensor
                     return_mode: str):
     """qflash_forward on the device: scales, constants, quantisation, bias,
     attention with the dequantisation fused, in stream order."""
-    scales, finish = quantize_qkv(query, key, value)           # kernel.py:294-296
-    # the constants need only the scales: on a side stream, beside the quantisation
-    params, _, join = _constants_beside(scales, scale, query.shape[2], query.shape[-1],
-                                        attn_mask is not None)  # kernel.py:297-307
+    # kernel.py:294-307: scales, then the constants from them (one kernel)
+    scales, params, finish = _hip_scales(query, key, value,
+                                         (scale, query.shape[2], query.shape[-1], attn_mask is not None))
     q8, k8, v8 = finish()                                       # kernel.py:309-311
-    join()
     return forward_codes(q8, k8, v8, scales, attn_mask, scale, return_mode, params=params)
 
 
@@ -712,13 +720,9 @@ def qflash_forward_window(query: Tensor, key: Tensor, value: Tensor, rel_bias: T
     if tables_fp32 and _device_path(query, key, value, None):
         if mask is not None and Z % mask.shape[0]:
             raise ValueError(f"batch {Z} is not a multiple of the {mask.shape[0]} windows of the mask")
-        scales, finish = quantize_qkv(query, key, value)
-        # the constants and the window bias need only the scales: on a side
-        # stream, beside the quantisation
-        params, wb, join = _constants_beside(scales, scale, N, d_q, True,
-                                             lambda p: window_bias_planned(rel_bias, mask, p))
+        scales, params, finish = _hip_scales(query, key, value, (scale, N, d_q, True))
+        wb = window_bias_planned(rel_bias, mask, params)
         q8, k8, v8 = finish()
-        join()
         check = _status_check(params)
         bias, zmod = (wb.expand(Z, H, N, N), 0) if mask is None else (wb, mask.shape[0])
         out = torch.empty_like(v8, dtype=scales.dtype)

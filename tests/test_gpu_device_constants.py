@@ -125,3 +125,42 @@ def test_forward_in_a_captured_graph():
         torch.cuda.synchronize()
         assert torch.equal(out, eager), rep
         _ = (q.sum() + 1).item()  # eager work between replays
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("masked", [False, True])
+def test_scales_constants_equal_the_two_calls(dtype, masked):
+    """qflash_hip_scales_constants (one kernel for the scales and the constants)
+    writes the scales and parameter block that qflash_hip_scales followed by
+    qflash_hip_constants write, and leaves its workspace zero, over inputs whose
+    products q_scale * k_scale land on different constants (and a zero tensor:
+    sm_scale 0, the ZeroDivisionError status)."""
+    import ctypes
+
+    from qflash_amd.kernel import _DT_CODE, _flags, quantize_qkv
+
+    L = _lib.load()
+    g = torch.Generator().manual_seed(7)
+    for trial, amp in enumerate((1.0, 3.7, 0.02, 40.0, 0.0)):
+        Z, H, N, D = 2, 3, 70 + 31 * trial, 64
+        q, k, v = ((torch.randn(Z, H, N, D, generator=g) * amp).to(dtype).to(DEV) for _ in range(3))
+        scale = (1.0 / math.sqrt(D)) * LOG2E
+        scales_a, _ = quantize_qkv(q, k, v)
+        params_a = device_constants(scales_a, scale, N, D, masked)
+        geo = (ctypes.c_int64 * 24)(*q.shape, *q.stride(), *k.shape, *k.stride(), *v.shape, *v.stride())
+        ws = torch.zeros(_lib.SCALES_WORKSPACE, dtype=torch.int32, device=DEV)
+        scales_b = torch.empty(4, dtype=dtype, device=DEV)
+        params_b = torch.empty(_lib.PARAMS_WORDS, dtype=torch.int32, device=DEV)
+        vp = ctypes.c_void_p
+        rc = L.qflash_hip_scales_constants(vp(q.data_ptr()), vp(k.data_ptr()), vp(v.data_ptr()), _DT_CODE[dtype],
+                                           geo, vp(scales_b.data_ptr()), vp(ws.data_ptr()), ws.numel(), scale, N, D,
+                                           int(masked), ctypes.byref(_flags()), vp(params_b.data_ptr()),
+                                           vp(torch.cuda.current_stream().cuda_stream))
+        assert rc == 0, L.qflash_hip_last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(scales_a.cpu().view(torch.int16 if dtype != torch.float32 else torch.int32),
+                           scales_b.cpu().view(torch.int16 if dtype != torch.float32 else torch.int32)), trial
+        assert params_a.cpu().tolist() == params_b.cpu().tolist(), trial
+        assert int(ws.abs().sum()) == 0
+        if amp == 0.0:
+            assert params_b[0].item() == _lib.STATUS_ZERODIV_SCALE
