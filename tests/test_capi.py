@@ -155,6 +155,22 @@ def test_quantiser_entries_check_arguments(lib):
     ost = (ctypes.c_int64 * 12)(*([128, 128, 32, 1] * 3))
     assert lib.qflash_hip_quantize(fake, fake, fake, _lib.F32, geo, None, fake, fake, ost, fake, None) == -1
     assert b"null" in lib.qflash_hip_last_error()
+    # the scales and constants entry checks both halves' arguments before any launch
+    fl = _lib.Flags(1, 1, 1, 30, 30)
+    params = ctypes.c_void_p(64)
+    assert lib.qflash_hip_scales_constants(fake, fake, fake, _lib.F32, geo, None, ws, _lib.SCALES_WORKSPACE, 0.18,
+                                           32, 32, 0, ctypes.byref(fl), params, None) == -1
+    assert b"null" in lib.qflash_hip_last_error()
+    assert lib.qflash_hip_scales_constants(fake, fake, fake, _lib.F32, geo, fake, ws, _lib.SCALES_WORKSPACE, 0.18,
+                                           0, 32, 0, ctypes.byref(fl), params, None) == -1
+    assert b"N_CTX" in lib.qflash_hip_last_error()
+    assert lib.qflash_hip_scales_constants(fake, fake, fake, _lib.F32, geo, fake, ws, 3, 0.18, 32, 32, 0,
+                                           ctypes.byref(fl), params, None) == -1
+    assert b"workspace" in lib.qflash_hip_last_error()
+    bad_fl = _lib.Flags(1, 1, 1, 0, 30)
+    assert lib.qflash_hip_scales_constants(fake, fake, fake, _lib.F32, geo, fake, ws, _lib.SCALES_WORKSPACE, 0.18,
+                                           32, 32, 0, ctypes.byref(bad_fl), params, None) == -1
+    assert b"l_shift" in lib.qflash_hip_last_error()
 
 
 def test_bias_entries_check_arguments(lib):
