@@ -423,6 +423,8 @@ def main(argv=None):
                     help="only the end-to-end op (warmup + steps calls, synchronised each) for rocprofv3 runs")
     ap.add_argument("--profile-proj", action="store_true",
                     help="only the int8 QKV projection (qkv_int8 at cfg3's shape), warmup + steps calls")
+    ap.add_argument("--graph", action="store_true",
+                    help="with --profile-e2e: replay the call captured in a HIP graph (after a settle phase)")
     ap.add_argument("--dense-bias", action="store_true",
                     help="with --profile-e2e on a Swin config: the materialised (B_, H, N, N) mask path")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MB",
@@ -452,6 +454,12 @@ def main(argv=None):
     if args.profile_proj:
         r = qkv_int8_block(dev, reps=max(1, args.steps))
         print(json.dumps(r), flush=True)
+        return 0
+    if args.profile_e2e and args.graph:
+        w = prepare(args.config, args.seed, dev, dense_bias=args.dense_bias)
+        us = e2e_graph_us(w, dev, reps=args.steps, settle_ms=args.settle_ms)
+        print(json.dumps({"config": args.config, "dense_bias": args.dense_bias, "steps": args.steps,
+                          "e2e_graph_us_median": us}), flush=True)
         return 0
     if args.profile_e2e:
         w = prepare(args.config, args.seed, dev, dense_bias=args.dense_bias)
