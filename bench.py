@@ -5,7 +5,8 @@ ViT-B/384 attention: B=64, H=12, N=577, d=64) with int8 Q/K/V already
 resident in HBM.  Prints ONE JSON line:
 
   value      int8 TOPS = 4*Z*H*N^2*D / (time per call)
-  roofline   the kernel's achieved TOPS (HIP events on its launch stream) vs
+  roofline   the kernel's achieved TOPS (HIP events around the timed launches,
+             on their launch stream) vs
              the int8 dense MFMA peak, plus HBM bytes per launch from
              rocprofv3 counters when a summary exists under profiles/
   cpu_baseline  the C oracle (OpenMP) on the host cores, same workload
@@ -126,23 +127,35 @@ def settle(step, ms: float) -> dict:
 
 
 def time_steps(step, steps: int, warmup: int):
-    """(wall ms per step, mean per-launch event ms, median per-launch event ms)."""
+    """(wall ms per step, mean launch ms, median per-launch event ms).
+    `steps` back-to-back launches with nothing between them, synchronised
+    before and after: the wall time per step, and the mean launch duration
+    from one pair of HIP events around the whole region on the launch stream
+    (torch's current stream, where make_step launches).  The median comes
+    from per-launch event pairs over a second run of `steps` launches."""
     import torch
 
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    r0.record()
+    for _ in range(steps):
+        step()
+    r1.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    region = r0.elapsed_time(r1) / steps
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    t0 = time.perf_counter()
     for i in range(steps):
         starts[i].record()
         step()
         ends[i].record()
     torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) * 1e3 / steps
     ev = [a.elapsed_time(b) for a, b in zip(starts, ends)]
-    return wall, sum(ev) / len(ev), statistics.median(ev)
+    return wall, region, statistics.median(ev)
 
 
 def sqnr_db(w, dev) -> float:
@@ -518,8 +531,9 @@ def main(argv=None):
         "sqnr_db": head["sqnr_db"],
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_INT8_TOPS, "unit": "TOPS",
                      "frac": achieved / PEAK_INT8_TOPS, "traffic": traffic,
-                     "note": "int8 tera-operations/s (2 ops per MAC, 4*Z*H*N^2*D per call, HIP events on the "
-                             "launch stream) vs 5.0 POPS dense int8 MFMA",
+                     "note": "int8 tera-operations/s (2 ops per MAC, 4*Z*H*N^2*D per call; mean launch "
+                             "duration from HIP events around the timed launches on the launch stream) vs "
+                             "5.0 POPS dense int8 MFMA",
                      "ops_per_launch": cfg_ops,
                      "roofline_us": head["roofline_us"], "roofline_frac": head["roofline_frac"],
                      "hbm_gbs_algorithmic": head["hbm_gbs_algorithmic"]},
