@@ -586,7 +586,7 @@ struct StageDma {
     static constexpr int NT = 64 * W;
     static constexpr int R = (S::SLOTS + NT - 1) / NT;
     uint32_t vk[R], vv[R];
-    __device__ StageDma(const Args& a, int wave, int lane) {
+    __device__ __forceinline__ StageDma(const Args& a, int wave, int lane) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const int slot = r * NT + wave * 64 + lane;
@@ -595,8 +595,8 @@ struct StageDma {
             vv[r] = (uint32_t)(key * (int32_t)a.sv[2] + 16 * (pos ^ S::vswz(key)));
         }
     }
-    __device__ void issue(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv, int8_t* buf, int kstart,
-                          const Args& a, int wave) const {
+    __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv, int8_t* buf,
+                                          int kstart, const Args& a, int wave) const {
         const uint32_t sk = (uint32_t)(kstart * (int32_t)a.sk[2]), sv = (uint32_t)(kstart * (int32_t)a.sv[2]);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -610,6 +610,21 @@ struct StageDma {
         }
     }
 };
+
+// The copy of a row block's first K / V stage into stage buffer 0 (fast_rows
+// builds the same buffers and offsets for the later stages), issued where it
+// is called: before the Q loads and the table fill, so their latencies overlap.
+template <int D, int W>
+__device__ __forceinline__ void first_stage(const Args& a, const int8_t* kb, const int8_t* vb, int8_t* smem,
+                                            int wave, int lane) {
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc((void*)kb, 0, (a.N - 1) * (int32_t)a.sk[2] + D, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc((void*)vb, 0, (a.N - 1) * (int32_t)a.sv[2] + D, 0x00020000);
+    const StageDma<D, W> dma(a, wave, lane);
+    dma.issue(rk, rv, smem, 0, a, wave);
+    asm volatile("" ::: "memory");
+}
 
 // Completion of this wave's LDS copies (vmcnt), then the workgroup barrier.
 __device__ __forceinline__ void stage_sync() {
@@ -1323,8 +1338,7 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
     const StageDma<D, W> dma(a, wave, lane);
     const Frag<D> fr(lane);
     const uint32_t lds0 = lds_addr(smem);  // a constant: the kernel's LDS array
-    dma.issue(rk, rv, smem, 0, a, wave);
-    stage_sync();
+    stage_sync();  // the first stage, issued by fast_block
 
     static_assert(S::BYTES >= W * 256, "epilogue slots of 256 bytes per wave in one stage buffer");
     const int nfull = a.N >> 5;
@@ -1417,9 +1431,22 @@ __device__ __forceinline__ void fast_rows(const Args& a, const i32x4* qv, int8_t
 template <int D>
 constexpr int fast_waves_per_simd() { return D <= 32 ? QF_FAST_WAVES_D32 : (D == 64 ? QF_FAST_WAVES_D64 : 2); }
 
+// The p(u) table at lut, entry lut_n - 1 - u (lut_pack_vt), and for masked
+// launches the far columns' constant at entry lut_n (lut_n + 1 <= kLutMax,
+// host); visible after fast_rows' first barrier.  lut_n - 1 <= x_safe (host),
+// where the 24-bit E is exact.
+template <int W, bool MASKED>
+__device__ __forceinline__ void fill_lut(const Args& a, int8_t* lut) {
+    for (int u = threadIdx.x; u < a.lut_n; u += 64 * W)
+        lut[a.lut_n - 1 - u] = (int8_t)(mad24(exp2_fast(-u, a.eM, a.rs), a.rM, 1 << 15) >> 16);
+    if constexpr (MASKED)
+        if (threadIdx.x == 0 && a.lut_n > 0) lut[a.lut_n] = (int8_t)a.far_p;
+}
+
 // One workgroup of the single-tile kernel: row block mb (32 * W rows) of head
-// zh, in the LDS array smem whose table the caller has filled (visible after
-// fast_rows' first barrier).
+// zh, in the LDS array smem.  The copy of the first K / V stage, the Q loads
+// and the table fill (visible after fast_rows' first barrier) go out before
+// any of them is waited for, so that their latencies overlap.
 template <int D, int W, bool MASKED, bool DYN>
 __device__ __forceinline__ void fast_block(const Args& a, int8_t* smem, int zh, int mb) {
     constexpr int DB = D / 32;
@@ -1434,6 +1461,7 @@ __device__ __forceinline__ void fast_block(const Args& a, int8_t* smem, int zh, 
     const int8_t* qb = a.q + z * a.sq[0] + h * a.sq[1];
     const int8_t* kb = a.k + z * a.sk[0] + h * a.sk[1];
     const int8_t* vb = a.v + z * a.sv[0] + h * a.sv[1];
+    first_stage<D, W>(a, kb, vb, smem, wave, lane);
     BiasRow brow;
     if constexpr (MASKED) {
         const int32_t* bh = a.bias + (a.bias_zmod ? z % a.bias_zmod : z) * a.sb[0] + h * a.sb[1];
@@ -1453,6 +1481,7 @@ __device__ __forceinline__ void fast_block(const Args& a, int8_t* smem, int zh, 
     for (int db = 0; db < DB; ++db)
         qv[db] = qrow < a.N ? *reinterpret_cast<const i32x4*>(qb + (int64_t)qrow * a.sq[2] + db * 32 + g * 16)
                             : i32x4{0, 0, 0, 0};
+    fill_lut<W, MASKED>(a, smem + 2 * Stage<D, W>::BYTES);
 
     // Unmasked: every real key column of this row has |s| <= 128*||q_row||_1, so
     // |x| = |s - m'| <= X_row for the scores and, past the first step, for
@@ -1508,23 +1537,11 @@ __device__ __forceinline__ void fast_block(const Args& a, int8_t* smem, int zh, 
     }
 }
 
-// The p(u) table at lut, entry lut_n - 1 - u (lut_pack_vt), and for masked
-// launches the far columns' constant at entry lut_n (lut_n + 1 <= kLutMax,
-// host); visible after fast_rows' first barrier.  lut_n - 1 <= x_safe (host),
-// where the 24-bit E is exact.
-template <int W, bool MASKED>
-__device__ __forceinline__ void fill_lut(const Args& a, int8_t* lut) {
-    for (int u = threadIdx.x; u < a.lut_n; u += 64 * W)
-        lut[a.lut_n - 1 - u] = (int8_t)(mad24(exp2_fast(-u, a.eM, a.rs), a.rM, 1 << 15) >> 16);
-    if constexpr (MASKED)
-        if (threadIdx.x == 0 && a.lut_n > 0) lut[a.lut_n] = (int8_t)a.far_p;
-}
 
 template <int D, int W, bool MASKED, bool DYN>
 __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Args a) {
     using S = Stage<D, W>;
     __shared__ __attribute__((aligned(16))) int8_t smem[2 * S::BYTES + kLutMax];
-    fill_lut<W, MASKED>(a, smem + 2 * S::BYTES);
     const int wg = xcd_order(blockIdx.x, a.n_wg);
     fast_block<D, W, MASKED, DYN>(a, smem, wg / a.mblocks, wg % a.mblocks);
 }
@@ -1544,7 +1561,6 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast_pla
     __shared__ __attribute__((aligned(16))) int8_t smem[2 * S::BYTES + kLutMax];
     if (a.params[kPStatus] != 0 || !a.params[kPFast] || !a.params[kPIdOk]) return;
     load_params(a);
-    fill_lut<W, MASKED>(a, smem + 2 * S::BYTES);
     const int wg = xcd_order(blockIdx.x, a.n_wg);
     fast_block<D, W, MASKED, false>(a, smem, wg / a.mblocks, wg % a.mblocks);
 }
@@ -1560,7 +1576,6 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_planned_
         general_block<D, W, MASKED, true>(a, xcd_order(blockIdx.x, a.n_wg), smem);
         return;
     }
-    fill_lut<W, MASKED>(a, smem + 2 * S::BYTES);
     const int wg = xcd_order(blockIdx.x, a.n_wg);
     fast_block<D, W, MASKED, true>(a, smem, wg / a.mblocks, wg % a.mblocks);
 }
