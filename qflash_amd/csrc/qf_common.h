@@ -30,6 +30,14 @@ __device__ __forceinline__ uint32_t qf_bf16_bits(float f) {
 }
 
 namespace qfs {
+// Workgroup id b of a grid of n -> logical id, so that consecutive logical ids
+// run on the same XCD (the hardware deals workgroups to the 8 XCDs round
+// robin: b runs on XCD b % 8, which gets one contiguous range of ids).
+__device__ __forceinline__ int xcd_order(int b, int n) {
+    const int per = n >> 3, rem = n & 7, x = b & 7, i = b >> 3;
+    return x < rem ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
+}
+
 constexpr int kScaleSlots = 64;  // absmax slots per tensor in the scales workspace
 static_assert(3 * kScaleSlots <= QFLASH_HIP_SCALES_WORKSPACE, "workspace: 3 x kScaleSlots partial maxima");
 

@@ -305,10 +305,7 @@ __device__ __forceinline__ void stage_kv(const Args& a, const int8_t* kb, const 
 // arithmetic on every element: exact for any constants and inputs.
 // Workgroup id -> (head, query block) so that consecutive blocks of one head
 // run on the same XCD (workgroups are dealt to the 8 XCDs round-robin).
-__device__ __forceinline__ int xcd_order(int b, int n) {
-    const int per = n >> 3, rem = n & 7, x = b & 7, i = b >> 3;
-    return x < rem ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
-}
+using qfs::xcd_order;
 
 // One workgroup of the general kernel: row block blk % mblocks of head
 // blk / mblocks, with LDS at smem (Tile<D>::BYTES).

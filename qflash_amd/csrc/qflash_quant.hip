@@ -533,10 +533,6 @@ struct ProjArgs {
     int8_t* out;
 };
 
-// 16 bytes at byte offset `off` of a buffer; past its end they read as 0
-__device__ __forceinline__ pi32x4 proj_load(__amdgpu_buffer_rsrc_t r, int32_t off) {
-    return __builtin_bit_cast(pi32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
 
 // One workgroup: a 128 x 128 tile of y, four waves of 64 x 64 (2 x 2 blocks of
 // v_mfma_i32_32x32x32_i8: lane l holds row l % 32 of x8 and of w8, 16 bytes of
@@ -550,51 +546,81 @@ __device__ inline float mul_add_rn(float a, float b, float c) {
     return a * b + c;
 }
 
+// The workgroup's 128 rows of x8 and 128 rows of w8 go through LDS in stages
+// of kProjK bytes of K, double-buffered: each thread copies its 16-byte chunks
+// HBM -> LDS with buffer_load ... lds (two per operand per stage), so the four
+// waves share every load; row r's chunk c sits at r * kProjK + 16 * (c ^ swz(r))
+// so that the ds_read_b128 of eight consecutive rows hit distinct banks.
+constexpr int kProjK = 64;                            // bytes of K per stage
+constexpr int kProjStage = 2 * kProjTile * kProjK;    // A and B tiles of one stage
+__device__ __forceinline__ int proj_swz(int r) { return (r >> 1) & 3; }
+
 template <int MODE>
 __global__ __launch_bounds__(256) void proj_kernel(ProjArgs p) {
+    __shared__ __attribute__((aligned(16))) int8_t lds[2 * kProjStage];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lr = lane & 31, g = lane >> 5;
-    const int m0 = blockIdx.x * kProjTile + (wave & 1) * 64;
-    const int n0 = blockIdx.y * kProjTile + (wave >> 1) * 64;
+    // tiles in XCD-aware order: the column tiles of one row tile run on one XCD,
+    // so its x8 rows come from HBM once into that XCD's L2
+    const int nct = (p.Nc + kProjTile - 1) / kProjTile;
+    const int tile = qfs::xcd_order(blockIdx.x, gridDim.x);
+    const int mt = (tile / nct) * kProjTile, nt = (tile % nct) * kProjTile;
+    const int m0 = mt + (wave & 1) * 64;
+    const int n0 = nt + (wave >> 1) * 64;
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)p.x8, 0, p.M * p.K, 0x00020000);
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)p.w8, 0, p.Nc * p.K, 0x00020000);
-    int32_t ao[2], bo[2];
+    // this thread's copy slots: slot s = 256 i + tid is row s / 4, stored chunk s % 4
+    int32_t ca[2], cb[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        ao[i] = (m0 + 32 * i + lr) * p.K + 16 * g;
-        bo[i] = (n0 + 32 * i + lr) * p.K + 16 * g;
+        const int sl = 256 * i + tid, r = sl >> 2, c = (sl & 3) ^ proj_swz(r);
+        ca[i] = (mt + r) * p.K + 16 * c;
+        cb[i] = (nt + r) * p.K + 16 * c;
+    }
+    auto issue = [&](int8_t* buf, int k0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            int8_t* la = buf + (256 * i + 64 * wave) * 16;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)la, 16, ca[i], k0,
+                                                     0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rw, (__attribute__((address_space(3))) void*)(la + kProjTile * kProjK), 16, cb[i], k0, 0, 0);
+        }
+    };
+    // LDS offsets of this lane's fragment rows (chunk 0); the chunk is xor-ed in per K step
+    int ra[2], rb[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        ra[i] = (wave & 1) * 64 + 32 * i + lr;
+        rb[i] = (wave >> 1) * 64 + 32 * i + lr;
     }
     pi32x16 acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = pi32x16{};
-    pi32x4 a[2], b[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        a[i] = proj_load(rx, ao[i]);
-        b[i] = proj_load(rw, bo[i]);
-    }
-    for (int k0 = 0; k0 < p.K; k0 += 32) {
-        pi32x4 an[2], bn[2];
-        const bool more = k0 + 32 < p.K;
-        if (more) {
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                an[i] = proj_load(rx, ao[i] + k0 + 32);
-                bn[i] = proj_load(rw, bo[i] + k0 + 32);
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
-        if (more) {
+    const int nst = (p.K + kProjK - 1) / kProjK;
+    issue(lds, 0);
+    for (int st = 0; st < nst; ++st) {
+        int8_t* buf = lds + (st & 1) * kProjStage;
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's copies of stage st
+        __syncthreads();                     // every copy of stage st; every read of stage st - 1
+        if (st + 1 < nst) issue(lds + ((st + 1) & 1) * kProjStage, (st + 1) * kProjK);
+        const int nk = min(kProjK, p.K - st * kProjK) / 32;  // 32-byte MFMA steps in this stage
+        for (int kk = 0; kk < nk; ++kk) {
+            const int c = 2 * kk + g;
+            pi32x4 a[2], b[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                a[i] = an[i];
-                b[i] = bn[i];
+                a[i] = *reinterpret_cast<const pi32x4*>(buf + ra[i] * kProjK + 16 * (c ^ proj_swz(ra[i])));
+                b[i] = *reinterpret_cast<const pi32x4*>(buf + kProjTile * kProjK + rb[i] * kProjK +
+                                                        16 * (c ^ proj_swz(rb[i])));
             }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], acc[i][j], 0, 0, 0);
         }
     }
     const float sx = *p.x_scale;
@@ -633,13 +659,13 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs p) {
         }
         if constexpr (MODE == 0) {
             mx = wave_max(mx);
-            if (lane == 0) atomicMax(p.ws + t * kSlots + (blockIdx.x + blockIdx.y * gridDim.x) % kSlots, mx);
+            if (lane == 0) atomicMax(p.ws + t * kSlots + blockIdx.x % kSlots, mx);
         }
     }
 }
 
 static int qkv_int8(const ProjArgs& pa, float* scales, hipStream_t st) {
-    const dim3 grid((unsigned)((pa.M + kProjTile - 1) / kProjTile), (unsigned)((pa.Nc + kProjTile - 1) / kProjTile));
+    const dim3 grid((unsigned)(((pa.M + kProjTile - 1) / kProjTile) * ((pa.Nc + kProjTile - 1) / kProjTile)));
     hipLaunchKernelGGL((proj_kernel<0>), grid, dim3(256), 0, st, pa);
     hipLaunchKernelGGL((scales_kernel<QFLASH_HIP_F32>), dim3(1), dim3(64), 0, st, pa.ws, (void*)scales);
     ProjArgs p1 = pa;
