@@ -548,12 +548,20 @@ __device__ inline float mul_add_rn(float a, float b, float c) {
 
 // The workgroup's 128 rows of x8 and 128 rows of w8 go through LDS in stages
 // of kProjK bytes of K, double-buffered: each thread copies its 16-byte chunks
-// HBM -> LDS with buffer_load ... lds (two per operand per stage), so the four
-// waves share every load; row r's chunk c sits at r * kProjK + 16 * (c ^ swz(r))
+// HBM -> LDS with buffer_load ... lds (kProjCopies per operand per stage), so
+// the four waves share every load; row r's chunk c sits at r * kProjK + 16 * (c ^ swz(r))
 // so that the ds_read_b128 of eight consecutive rows hit distinct banks.
-constexpr int kProjK = 64;                            // bytes of K per stage
+#ifndef QF_PROJ_K
+#define QF_PROJ_K 64
+#endif
+constexpr int kProjK = QF_PROJ_K;                     // bytes of K per stage (64 or 128)
+constexpr int kProjCpr = kProjK / 16;                 // 16-byte chunks per row
+constexpr int kProjCopies = kProjTile * kProjCpr / 256;  // chunks per thread and operand
 constexpr int kProjStage = 2 * kProjTile * kProjK;    // A and B tiles of one stage
-__device__ __forceinline__ int proj_swz(int r) { return (r >> 1) & 3; }
+static_assert(kProjK == 64 || kProjK == 128, "stages of 64 or 128 bytes of K");
+// chunk position of row r: eight consecutive rows at one chunk land in the
+// eight 16-byte bank groups
+__device__ __forceinline__ int proj_swz(int r) { return kProjCpr == 4 ? (r >> 1) & 3 : r & 7; }
 
 template <int MODE>
 __global__ __launch_bounds__(256) void proj_kernel(ProjArgs p) {
@@ -569,17 +577,17 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs p) {
     const int n0 = nt + (wave >> 1) * 64;
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)p.x8, 0, p.M * p.K, 0x00020000);
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)p.w8, 0, p.Nc * p.K, 0x00020000);
-    // this thread's copy slots: slot s = 256 i + tid is row s / 4, stored chunk s % 4
-    int32_t ca[2], cb[2];
+    // this thread's copy slots: slot s = 256 i + tid is row s / kProjCpr, stored chunk s % kProjCpr
+    int32_t ca[kProjCopies], cb[kProjCopies];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int sl = 256 * i + tid, r = sl >> 2, c = (sl & 3) ^ proj_swz(r);
+    for (int i = 0; i < kProjCopies; ++i) {
+        const int sl = 256 * i + tid, r = sl / kProjCpr, c = (sl % kProjCpr) ^ proj_swz(r);
         ca[i] = (mt + r) * p.K + 16 * c;
         cb[i] = (nt + r) * p.K + 16 * c;
     }
     auto issue = [&](int8_t* buf, int k0) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < kProjCopies; ++i) {
             int8_t* la = buf + (256 * i + 64 * wave) * 16;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)la, 16, ca[i], k0,
                                                      0, 0);
