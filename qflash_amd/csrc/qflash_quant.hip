@@ -519,7 +519,13 @@ static uint32_t* scratch_ptr(int dev) {
 // scales kernel forms the scales, pass 1 recomputes y and stores the codes.
 typedef int32_t pi32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t pi32x16 __attribute__((ext_vector_type(16)));
-constexpr int kProjTile = 128;  // rows (tokens) and columns (output channels) per workgroup
+#ifndef QF_PROJ_TM
+#define QF_PROJ_TM 128
+#endif
+constexpr int kProjTile = 128;         // columns (output channels) per workgroup
+constexpr int kProjTM = QF_PROJ_TM;    // rows (tokens) per workgroup: 128 or 256
+constexpr int kProjWaves = kProjTM / 32;  // waves of 64 x 64: kProjTM / 64 row groups x 2 column groups
+constexpr int kProjThreads = 64 * kProjWaves;
 
 struct ProjArgs {
     const int8_t* x8;
@@ -556,51 +562,61 @@ __device__ inline float mul_add_rn(float a, float b, float c) {
 #endif
 constexpr int kProjK = QF_PROJ_K;                     // bytes of K per stage (64 or 128)
 constexpr int kProjCpr = kProjK / 16;                 // 16-byte chunks per row
-constexpr int kProjCopies = kProjTile * kProjCpr / 256;  // chunks per thread and operand
-constexpr int kProjStage = 2 * kProjTile * kProjK;    // A and B tiles of one stage
+constexpr int kProjCopiesA = kProjTM * kProjCpr / kProjThreads;    // chunks per thread of x8
+constexpr int kProjCopiesB = kProjTile * kProjCpr / kProjThreads;  // and of w8
+constexpr int kProjStage = (kProjTM + kProjTile) * kProjK;         // A and B tiles of one stage
 static_assert(kProjK == 64 || kProjK == 128, "stages of 64 or 128 bytes of K");
 // chunk position of row r: eight consecutive rows at one chunk land in the
 // eight 16-byte bank groups
 __device__ __forceinline__ int proj_swz(int r) { return kProjCpr == 4 ? (r >> 1) & 3 : r & 7; }
 
 template <int MODE>
-__global__ __launch_bounds__(256) void proj_kernel(ProjArgs p) {
+__global__ __launch_bounds__(kProjThreads) void proj_kernel(ProjArgs p) {
     __shared__ __attribute__((aligned(16))) int8_t lds[2 * kProjStage];
+    constexpr int RG = kProjTM / 64;  // row groups of waves
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lr = lane & 31, g = lane >> 5;
     // tiles in XCD-aware order: the column tiles of one row tile run on one XCD,
     // so its x8 rows come from HBM once into that XCD's L2
     const int nct = (p.Nc + kProjTile - 1) / kProjTile;
     const int tile = qfs::xcd_order(blockIdx.x, gridDim.x);
-    const int mt = (tile / nct) * kProjTile, nt = (tile % nct) * kProjTile;
-    const int m0 = mt + (wave & 1) * 64;
-    const int n0 = nt + (wave >> 1) * 64;
+    const int mt = (tile / nct) * kProjTM, nt = (tile % nct) * kProjTile;
+    const int m0 = mt + (wave % RG) * 64;
+    const int n0 = nt + (wave / RG) * 64;
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)p.x8, 0, p.M * p.K, 0x00020000);
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)p.w8, 0, p.Nc * p.K, 0x00020000);
-    // this thread's copy slots: slot s = 256 i + tid is row s / kProjCpr, stored chunk s % kProjCpr
-    int32_t ca[kProjCopies], cb[kProjCopies];
+    // this thread's copy slots: slot s = kProjThreads i + tid is row s / kProjCpr,
+    // stored chunk s % kProjCpr (A tile first, then the B tile at kProjTM * kProjK)
+    int32_t ca[kProjCopiesA], cb[kProjCopiesB];
 #pragma unroll
-    for (int i = 0; i < kProjCopies; ++i) {
-        const int sl = 256 * i + tid, r = sl / kProjCpr, c = (sl % kProjCpr) ^ proj_swz(r);
+    for (int i = 0; i < kProjCopiesA; ++i) {
+        const int sl = kProjThreads * i + tid, r = sl / kProjCpr, c = (sl % kProjCpr) ^ proj_swz(r);
         ca[i] = (mt + r) * p.K + 16 * c;
+    }
+#pragma unroll
+    for (int i = 0; i < kProjCopiesB; ++i) {
+        const int sl = kProjThreads * i + tid, r = sl / kProjCpr, c = (sl % kProjCpr) ^ proj_swz(r);
         cb[i] = (nt + r) * p.K + 16 * c;
     }
     auto issue = [&](int8_t* buf, int k0) {
 #pragma unroll
-        for (int i = 0; i < kProjCopies; ++i) {
-            int8_t* la = buf + (256 * i + 64 * wave) * 16;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)la, 16, ca[i], k0,
-                                                     0, 0);
+        for (int i = 0; i < kProjCopiesA; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rw, (__attribute__((address_space(3))) void*)(la + kProjTile * kProjK), 16, cb[i], k0, 0, 0);
-        }
+                rx, (__attribute__((address_space(3))) void*)(buf + (kProjThreads * i + 64 * wave) * 16), 16, ca[i],
+                k0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < kProjCopiesB; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rw,
+                (__attribute__((address_space(3))) void*)(buf + kProjTM * kProjK + (kProjThreads * i + 64 * wave) * 16),
+                16, cb[i], k0, 0, 0);
     };
     // LDS offsets of this lane's fragment rows (chunk 0); the chunk is xor-ed in per K step
     int ra[2], rb[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        ra[i] = (wave & 1) * 64 + 32 * i + lr;
-        rb[i] = (wave >> 1) * 64 + 32 * i + lr;
+        ra[i] = (wave % RG) * 64 + 32 * i + lr;
+        rb[i] = (wave / RG) * 64 + 32 * i + lr;
     }
     pi32x16 acc[2][2];
 #pragma unroll
@@ -621,7 +637,7 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs p) {
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 a[i] = *reinterpret_cast<const pi32x4*>(buf + ra[i] * kProjK + 16 * (c ^ proj_swz(ra[i])));
-                b[i] = *reinterpret_cast<const pi32x4*>(buf + kProjTile * kProjK + rb[i] * kProjK +
+                b[i] = *reinterpret_cast<const pi32x4*>(buf + kProjTM * kProjK + rb[i] * kProjK +
                                                         16 * (c ^ proj_swz(rb[i])));
             }
 #pragma unroll
@@ -673,12 +689,12 @@ __global__ __launch_bounds__(256) void proj_kernel(ProjArgs p) {
 }
 
 static int qkv_int8(const ProjArgs& pa, float* scales, hipStream_t st) {
-    const dim3 grid((unsigned)(((pa.M + kProjTile - 1) / kProjTile) * ((pa.Nc + kProjTile - 1) / kProjTile)));
-    hipLaunchKernelGGL((proj_kernel<0>), grid, dim3(256), 0, st, pa);
+    const dim3 grid((unsigned)(((pa.M + kProjTM - 1) / kProjTM) * ((pa.Nc + kProjTile - 1) / kProjTile)));
+    hipLaunchKernelGGL((proj_kernel<0>), grid, dim3(kProjThreads), 0, st, pa);
     hipLaunchKernelGGL((scales_kernel<QFLASH_HIP_F32>), dim3(1), dim3(64), 0, st, pa.ws, (void*)scales);
     ProjArgs p1 = pa;
     p1.scales = scales;
-    hipLaunchKernelGGL((proj_kernel<1>), grid, dim3(256), 0, st, p1);
+    hipLaunchKernelGGL((proj_kernel<1>), grid, dim3(kProjThreads), 0, st, p1);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : fail(QFLASH_HIP_ELAUNCH, "launch failed: %s", hipGetErrorString(e));
 }
@@ -731,7 +747,9 @@ int qflash_hip_qkv_int8(const int8_t* x8, const int8_t* w8, const float* w_scale
     if (M < 1 || K < 32 || K % 32 || Nc < 96 || Nc % 96)
         return qfq::fail(QFLASH_HIP_EINVAL, "shape M=%d K=%d Nc=%d: need M >= 1, K a multiple of 32, Nc = 3 C with C a "
                          "multiple of 32", M, K, Nc);
-    if ((int64_t)M * K > INT32_MAX - 64 || (int64_t)Nc * K > INT32_MAX - 64 || (int64_t)(M + 127) * Nc > INT32_MAX)
+    // byte offsets of the GEMM's loads and stores (rows up to the last tile's end) in 31 bits
+    if ((int64_t)(M + 255) * K > INT32_MAX - 64 || (int64_t)(Nc + 127) * K > INT32_MAX - 64 ||
+        (int64_t)(M + 255) * Nc > INT32_MAX)
         return qfq::fail(QFLASH_HIP_EINVAL, "operands beyond 2 GiB");
     if (workspace_elems < QFLASH_HIP_SCALES_WORKSPACE)
         return qfq::fail(QFLASH_HIP_EINVAL, "workspace holds %lld entries, %d needed", (long long)workspace_elems,
