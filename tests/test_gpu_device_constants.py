@@ -89,6 +89,39 @@ def test_planned_forward_equals_host_constant_forward(masked):
     assert torch.equal(out.cpu(), o.cpu().float() * vs)
 
 
+@pytest.mark.parametrize("plan", ["exp_idiv", "l_idiv", "acc_idiv", "dynamic_bound", "long_rows"])
+def test_planned_forward_on_every_plan(monkeypatch, hip_hooks, plan):
+    """The planned attention is two launches, each of which runs only when the
+    device plan selects it: fwd_fast_planned (the fast path with the identity
+    proof of the rescale) and fwd_planned_rest (the per-row bound variant or
+    the general path).  Plans that send the work to the second one: the idiv
+    variants of kernel.py:30-36 (general path), the dynamic-bound hook (per-row
+    bound) and rows of 4096 keys (where the identity proof usually fails);
+    qflash.forward must equal the launch on host constants code for code."""
+    from qflash_amd import kernel as K
+    from qflash_amd.kernel import fixed_point_constants, launch_forward, quantize
+    N = 4096 if plan == "long_rows" else 197
+    flags = dict(EXP_USE_SHIFT=True, L_USE_SHIFT=True, ACC_USE_SHIFT=True, L_SHIFT=30, ACC_SHIFT=30)
+    name = {"exp_idiv": "EXP_USE_SHIFT", "l_idiv": "L_USE_SHIFT", "acc_idiv": "ACC_USE_SHIFT"}.get(plan)
+    if name:
+        monkeypatch.setattr(K, name, False)
+        flags[name] = False
+    if plan == "dynamic_bound":
+        hip_hooks("FORCE_DYNAMIC_BOUND")
+    g = torch.Generator().manual_seed(21)
+    Z, H, D = (1, 2, 64) if plan == "long_rows" else (2, 3, 64)
+    q, k, v = (torch.randn(Z, H, N, D, generator=g) for _ in range(3))
+    out = qflash.forward(q.to(DEV), k.to(DEV), v.to(DEV))
+    qs, ks, vs = (x.abs().amax() / 127 for x in (q, k, v))
+    sm = (1.0 / math.sqrt(D)) * LOG2E * (qs * ks).item()
+    c = fixed_point_constants(sm, 30, 30)
+    q8, k8, v8 = (quantize(x, s).to(DEV) for x, s in ((q, qs), (k, ks), (v, vs)))
+    o = torch.empty_like(v8)
+    launch_forward(q8, k8, v8, o, c, flags)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), o.cpu().float() * vs)
+
+
 def test_forward_raises_where_the_reference_raises():
     z = torch.zeros(1, 2, 40, 32, device=DEV)
     x = torch.randn(1, 2, 40, 32, device=DEV)
