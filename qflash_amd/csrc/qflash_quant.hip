@@ -116,6 +116,17 @@ __device__ __forceinline__ int8_t quant1_rcp(float x, float s, float r) {
     return quant1<QFLASH_HIP_F32>(x, s);
 }
 
+// quant1_rcp's fast path alone: the code, and in exact whether it equals
+// quant1's (false: the element needs the IEEE division, NaN included)
+__device__ __forceinline__ int32_t quant1_rcp_try(float x, float r, bool& exact) {
+    const float q0 = x * r;
+    const float n = rintf(q0);
+    const bool big = fabsf(q0) >= 130.0f;
+    exact = big || 0.5f - fabsf(q0 - n) > 0x1p-14f;
+    const float c = big ? (q0 > 0.f ? 127.0f : -128.0f) : fminf(fmaxf(n, -128.0f), 127.0f);
+    return (int32_t)c;
+}
+
 struct GeoSet {
     Geo g[3];  // q, k, v
 };
@@ -668,16 +679,49 @@ __global__ __launch_bounds__(kProjThreads) void proj_kernel(ProjArgs p) {
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
+            // y of result register v (row m0 + 32 i + 8 (v / 4) + 4 g + v % 4, column n)
+            auto yv = [&](int v) {
+                return p.bias ? mul_add_rn((float)acc[i][j][v], gsc, bb) : (float)acc[i][j][v] * gsc;
+            };
+            if constexpr (MODE == 0) {
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int m = m0 + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3);
-                const float y = p.bias ? mul_add_rn((float)acc[i][j][v], gsc, bb) : (float)acc[i][j][v] * gsc;
-                if constexpr (MODE == 0) {
-                    if (m < p.M) mx = max(mx, __float_as_uint(y) & 0x7fffffffu);
-                } else {
-                    const int8_t c = rcp_ok ? quant1_rcp(y, s, rcp) : quant1<QFLASH_HIP_F32>(y, s);
+                for (int v = 0; v < 16; ++v) {
+                    const uint32_t ay = __float_as_uint(yv(v)) & 0x7fffffffu;
+                    if (m0 + 32 * i + 8 * (v >> 2) + 4 * g + (v & 3) < p.M) mx = max(mx, ay);
+                }
+            } else {
+#pragma unroll
+                for (int v4 = 0; v4 < 4; ++v4) {
+                    // codes of registers 4 v4 .. 4 v4 + 3 (rows m0 + 32 i + 8 v4 + 4 g + r
+                    // of column n, byte r) through the reciprocal with no branch per
+                    // element; the few near a half-integer (all of them without a
+                    // usable reciprocal) are redone with the IEEE division
+                    uint32_t packed = 0, slow = rcp_ok ? 0u : 0xfu;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        bool ok;
+                        const int32_t c = quant1_rcp_try(yv(4 * v4 + r), rcp, ok);
+                        packed |= (uint32_t)(c & 0xff) << (8 * r);
+                        slow |= ok ? 0u : 1u << r;
+                    }
+                    if (slow) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (slow >> r & 1) {
+                                const uint32_t c = (uint8_t)quant1<QFLASH_HIP_F32>(yv(4 * v4 + r), s);
+                                packed = (packed & ~(0xffu << (8 * r))) | c << (8 * r);
+                            }
+                    }
+                    // 4 x 4 byte transpose over the lane quad (columns 4a .. 4a + 3): lane
+                    // 4a + b then holds row m0 + 32 i + 8 v4 + 4 g + b of those four columns
+                    const int b = lr & 3;
+                    const uint32_t x = (uint32_t)__builtin_amdgcn_mov_dpp((int)packed, 0xB1, 0xF, 0xF, false);
+                    const uint32_t h = __builtin_amdgcn_perm(x, packed, (b & 1) ? 0x03070105u : 0x06020400u);
+                    const uint32_t y = (uint32_t)__builtin_amdgcn_mov_dpp((int)h, 0x4E, 0xF, 0xF, false);
+                    const uint32_t row = __builtin_amdgcn_perm(y, h, (b & 2) ? 0x03020706u : 0x05040100u);
+                    const int m = m0 + 32 * i + 8 * v4 + 4 * g + b;
                     // rows >= M lie past the buffer's end: the store is dropped
-                    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)c, ro, m * p.Nc + n, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b32(row, ro, m * p.Nc + nb + 4 * (lr >> 2), 0, 0);
                 }
             }
         }
