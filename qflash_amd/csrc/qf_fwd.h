@@ -27,6 +27,7 @@
 //                      col l%32)
 //   (checked at run time by qflash_hip_mfma_layout_check).
 #pragma once
+#include <cstring>
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 #include <atomic>
@@ -98,6 +99,19 @@ struct Args {
     const int32_t* params;
     int32_t general_only;  // with params: the general kernel runs whatever the plan says (layout)
 };
+
+// The p(u) table of a launch on host constants, formed by the host and passed
+// with the kernel arguments (fwd_fast_table: the workgroups copy it into LDS
+// instead of computing it) when it holds at most 4 kLutArgWords bytes and
+// rows have at most 64 keys (two key steps per wave, where the table's
+// arithmetic is a large part of a wave: cfg4 -4 % measured on MI355X).
+constexpr int kLutArgWords = 256;
+struct LutArg {
+    uint32_t w[kLutArgWords];
+};
+__host__ __device__ __forceinline__ bool lut_in_args(const Args& a) {
+    return a.lut_n > 0 && a.lut_n < 4 * kLutArgWords && a.N <= 64;
+}
 
 // Words of the device parameter block written by qflash_hip_constants.
 enum ParamWord : int {
@@ -1430,8 +1444,33 @@ constexpr int fast_waves_per_simd() { return D <= 32 ? QF_FAST_WAVES_D32 : (D ==
 
 // The p(u) table at lut, entry lut_n - 1 - u (lut_pack_vt), and for masked
 // launches the far columns' constant at entry lut_n (lut_n + 1 <= kLutMax,
-// host); visible after fast_rows' first barrier.  lut_n - 1 <= x_safe (host),
-// where the 24-bit E is exact.
+// host); visible after fast_rows' first barrier.  Launches of fwd_fast_table
+// (lut_in_args: host constants, short rows) pass the bytes with the kernel
+// arguments (copy_lut, whole 256-byte chunks, at most 4 kLutArgWords <=
+// kLutMax bytes); otherwise the workgroup forms them (fill_lut), exact with
+// the 24-bit E since lut_n - 1 <= x_safe (host).  Entries past the table are
+// never read.
+template <int W, bool MASKED>
+__device__ __forceinline__ int lut_dwords(const Args& a) {
+    return a.lut_n > 0 ? (a.lut_n + (MASKED ? 4 : 3)) >> 2 : 0;
+}
+
+// pre: the host's table, copied to LDS by buffer_load ... lds (wave c
+// copies dwords 64 c .. 64 c + 63; those past the table read 0), visible, like
+// the first K / V stage, after fast_rows' first wait and barrier.  Issued
+// before the stage copy, with no LDS write of its own: an LDS store after an
+// LDS-bound load waits for every outstanding load.
+template <int W, bool MASKED>
+__device__ __forceinline__ void copy_lut(const Args& a, int8_t* lut, const uint32_t* pre, int wave, int lane) {
+    const int nd = lut_dwords<W, MASKED>(a);
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)pre, 0, nd * 4, 0x00020000);
+    for (int c = wave; 64 * c < nd; c += W)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(lut + 256 * c), 4,
+                                                 256 * c + 4 * lane, 0, 0, 0);
+}
+
+// nullptr pre: the workgroup forms the entries (a dword a lane measured slower
+// than a byte a lane, cfg1-3 +0.5-1.5 %)
 template <int W, bool MASKED>
 __device__ __forceinline__ void fill_lut(const Args& a, int8_t* lut) {
     for (int u = threadIdx.x; u < a.lut_n; u += 64 * W)
@@ -1445,7 +1484,8 @@ __device__ __forceinline__ void fill_lut(const Args& a, int8_t* lut) {
 // and the table fill (visible after fast_rows' first barrier) go out before
 // any of them is waited for, so that their latencies overlap.
 template <int D, int W, bool MASKED, bool DYN>
-__device__ __forceinline__ void fast_block(const Args& a, int8_t* smem, int zh, int mb) {
+__device__ __forceinline__ void fast_block(const Args& a, int8_t* smem, int zh, int mb,
+                                           const uint32_t* lut_pre = nullptr) {
     constexpr int DB = D / 32;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -1455,6 +1495,7 @@ __device__ __forceinline__ void fast_block(const Args& a, int8_t* smem, int zh, 
     const bool active = q0 < a.N;
     const int qrow = q0 + lq;
 
+    if (lut_pre) copy_lut<W, MASKED>(a, smem + 2 * Stage<D, W>::BYTES, lut_pre, wave, lane);
     const int8_t* qb = a.q + z * a.sq[0] + h * a.sq[1];
     const int8_t* kb = a.k + z * a.sk[0] + h * a.sk[1];
     const int8_t* vb = a.v + z * a.sv[0] + h * a.sv[1];
@@ -1478,7 +1519,7 @@ __device__ __forceinline__ void fast_block(const Args& a, int8_t* smem, int zh, 
     for (int db = 0; db < DB; ++db)
         qv[db] = qrow < a.N ? *reinterpret_cast<const i32x4*>(qb + (int64_t)qrow * a.sq[2] + db * 32 + g * 16)
                             : i32x4{0, 0, 0, 0};
-    fill_lut<W, MASKED>(a, smem + 2 * Stage<D, W>::BYTES);
+    if (!lut_pre) fill_lut<W, MASKED>(a, smem + 2 * Stage<D, W>::BYTES);
 
     // Unmasked: every real key column of this row has |s| <= 128*||q_row||_1, so
     // |x| = |s - m'| <= X_row for the scores and, past the first step, for
@@ -1541,6 +1582,23 @@ __global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast(Arg
     __shared__ __attribute__((aligned(16))) int8_t smem[2 * S::BYTES + kLutMax];
     const int wg = xcd_order(blockIdx.x, a.n_wg);
     fast_block<D, W, MASKED, DYN>(a, smem, wg / a.mblocks, wg % a.mblocks);
+}
+
+// fwd_fast for short rows (lut_in_args) with the table formed by the host.  A
+// kernel of its own: the table's kilobyte of arguments, on every launch of
+// fwd_fast, measured slower where the table is computed anyway (cfg3 +3 %).
+template <int D, int W, bool MASKED>
+__global__ __launch_bounds__(64 * W, fast_waves_per_simd<D>()) void fwd_fast_table(Args a, LutArg) {
+    using S = Stage<D, W>;
+    __shared__ __attribute__((aligned(16))) int8_t smem[2 * S::BYTES + kLutMax];
+    // the table argument, read in place in the kernel-argument segment (where
+    // the ABI puts it, right after `a`): indexing the by-value parameter would
+    // copy it to scratch memory first
+    static_assert(sizeof(Args) % alignof(LutArg) == 0, "LutArg follows Args in the kernel-argument segment");
+    const uint32_t* pre =
+        reinterpret_cast<const uint32_t*>((const char*)__builtin_amdgcn_kernarg_segment_ptr() + sizeof(Args));
+    const int wg = xcd_order(blockIdx.x, a.n_wg);
+    fast_block<D, W, MASKED, false>(a, smem, wg / a.mblocks, wg % a.mblocks, pre);
 }
 
 // The kernels on constants in device memory (qflash_hip_constants), for
@@ -1621,10 +1679,40 @@ static size_t lds_pad_for(Kern kern, int block, int k, std::atomic<int>* cache) 
     return (size_t)pad;
 }
 
+// The bytes fill_lut forms (lut_in_args(a)), from the reference's own
+// integer primitives: entry lut_n - 1 - u = p(u), then (masked) far_p.  Kept
+// per thread for the last constants, which repeat from call to call.
+static void lut_table(const Args& a, bool masked, LutArg* tb) {
+    struct Key {
+        int32_t rs, eM, rM, exp_mode, lut_n, far_p, masked;
+    };
+    thread_local Key last{};
+    thread_local LutArg table;
+    thread_local bool have = false;
+    const Key k{a.rs, a.eM, a.rM, a.exp_mode, a.lut_n, masked ? a.far_p : 0, masked ? 1 : 0};
+    if (!have || memcmp(&k, &last, sizeof k) != 0) {
+        uint8_t* b = reinterpret_cast<uint8_t*>(table.w);
+        memset(b, 0, sizeof table.w);
+        for (int j = 0; j < a.lut_n; ++j) b[j] = (uint8_t)(int8_t)requant(exp2_i32(-(a.lut_n - 1 - j), a), a);
+        if (masked) b[a.lut_n] = (uint8_t)(int8_t)a.far_p;
+        last = k;
+        have = true;
+    }
+    *tb = table;
+}
+
 template <int D, int W, bool MASKED, bool DYN>
 static hipError_t launch_fast(const Args& a, int wg_per_cu, dim3 grid, hipStream_t st) {
     static std::atomic<int> kmax_cache{0};
     static std::atomic<int> pad_cache[9] = {-1, -1, -1, -1, -1, -1, -1, -1, -1};
+    if constexpr (!DYN) {
+        if (lut_in_args(a) && wg_per_cu <= 0) {  // (the occupancy hook pads fwd_fast's LDS)
+            LutArg tb;
+            lut_table(a, MASKED, &tb);
+            hipLaunchKernelGGL((fwd_fast_table<D, W, MASKED>), grid, dim3(64 * W), 0, st, a, tb);
+            return hipGetLastError();
+        }
+    }
     auto kern = fwd_fast<D, W, MASKED, DYN>;
     int kmax = kmax_cache.load(std::memory_order_relaxed);
     if (kmax <= 0) {
