@@ -19,8 +19,11 @@
  *     default stream); the call returns 0 or a negative QFLASH_HIP_E* code
  *     and never throws; qflash_hip_last_error() gives a message for the
  *     last failure on the calling thread;
- *   - reentrant: no mutable global state besides the per-thread message and
- *     the test-hook bits of qflash_hip_set_test_hooks.
+ *   - reentrant: no mutable global state besides the per-thread message, a
+ *     per-thread copy of the last exp2 table formed on the host (a value of
+ *     the call's constants), per-process caches filled on first use
+ *     (occupancy, device addresses) and the test-hook bits of
+ *     qflash_hip_set_test_hooks.
  */
 #ifndef QFLASH_HIP_H
 #define QFLASH_HIP_H
